@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the GPA-VGGT merging hot path on one MI355X.
+
+One step = one fused similarity-argmax call on the 75,000 x 25,000 x 128
+workload plus one biased-attention call on the 200-frame merged-block
+workload (16 heads, 274,800 queries, 68,700 merged keys, head_dim 64), both
+on synthetic inputs already resident in HBM.  `value` is the step's
+algorithmic TFLOP/s (2*M*N*D for the similarity, 4*BH*M*N*D for attention).
+The JSON line also carries per-kernel ms / TFLOP/s / % of the bf16 dense
+MFMA peak, the reference 200-frame shapes, the roofline of the dominant
+kernel and a CPU baseline (the torch restatement of the reference path, timed
+on a bounded sample on this host).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "gpa-vggt_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2516.6     # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+SM_SCALE = 64 ** -0.5
+TRAFFIC_FILE = REPO / "profiles" / "attn_keybias_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description="GPA-VGGT merging hot path benchmark (1 GPU)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-200f", action="store_true", help="skip the 200-frame shape sweep")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of CPU work per baseline leg (similarity, attention)")
+    return ap.parse_args(argv)
+
+
+def event_ms(fn, reps: int):
+    """Per-call device time (ms) from events on torch's current stream."""
+    import torch
+    out = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        out.append((s, e))
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in out]
+
+
+def kernel_entry(flops: float, ms: float) -> dict:
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
+            "flops": flops}
+
+
+def cpu_baseline(src, dst, q, k, v, bias, budget: float) -> dict:
+    """Reference torch path on the host, on a bounded sample of the same workload."""
+    import torch
+    import gpa_workloads as W
+    from oracle.attention import sdpa_reference
+    from oracle.similarity import fast_similarity_chunks
+
+    threads = torch.get_num_threads()
+    a_h, b_h = src.cpu(), dst.cpu()
+    m_full, n_sim, d_sim = a_h.shape[1], b_h.shape[1], a_h.shape[2]
+    bt = b_h.transpose(1, 2)
+
+    def sim_rows(rows):
+        t = time.perf_counter()
+        fast_similarity_chunks(a_h[:, :rows], bt, 5000)
+        return time.perf_counter() - t
+
+    rows = 1000
+    dt = sim_rows(rows)
+    rows = int(min(m_full, max(rows, rows * budget / max(dt, 1e-3))))
+    dt = sim_rows(rows)
+    sim_rate = W.sim_flops(1, rows, n_sim, d_sim) / dt
+
+    qh = q[:, :, :4096].float().cpu()
+    kh, vh, bh = k.float().cpu(), v.float().cpu(), bias.float().cpu()
+    H, n_attn, d = kh.shape[1], kh.shape[2], kh.shape[3]
+
+    def attn_rows(rows):
+        t = time.perf_counter()
+        sdpa_reference(qh[:, :, :rows], kh, vh, bh, SM_SCALE)
+        return time.perf_counter() - t
+
+    qrows = 16
+    dt = attn_rows(qrows)
+    qrows = int(min(4096, max(qrows, qrows * budget / max(dt, 1e-3))))
+    dt = attn_rows(qrows)
+    attn_rate = W.attn_flops(H, qrows, n_attn, d) / dt
+
+    f_sim = W.sim_flops(1, m_full, n_sim, d_sim)
+    f_attn = W.attn_flops(H, q.shape[2], n_attn, d)
+    value = (f_sim + f_attn) / (f_sim / sim_rate + f_attn / attn_rate) / 1e12
+    return {
+        "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"torch CPU restatement of the reference path: fast_similarity_chunks "
+                   f"(bf16 bmm+max, chunk 5000) on {rows} of {m_full} source rows "
+                   f"({sim_rate / 1e12:.4f} TFLOP/s), fp32 SDPA with the log-count bias on "
+                   f"{qrows} of {q.shape[2]} queries x {H} heads x {n_attn} keys "
+                   f"({attn_rate / 1e12:.4f} TFLOP/s); per-step time extrapolated linearly "
+                   f"(rows are independent)"),
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the merging hot path has no multi-GPU path here "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
+        return 2
+
+    import torch
+    import gpa_workloads as W
+    from merging import _native
+    from merging.fused_attention import attention_keybias
+    from merging.fused_similarity import fused_similarity_argmax
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"[bench] device {torch.cuda.get_device_name(dev)}; library {_native.LIB_PATH}")
+
+    src, dst = W.sim_inputs(m=75_000, n=25_000, seed=0, device=dev)
+    q, k, v, bias = W.attn_inputs(m=274_800, n=68_700, seed=0, device=dev)
+    torch.cuda.synchronize()
+    f_sim = W.sim_flops(1, src.shape[1], dst.shape[1], src.shape[2])
+    f_attn = W.attn_flops(q.shape[1], q.shape[2], k.shape[2], q.shape[3])
+
+    def sim():
+        return fused_similarity_argmax(src, dst)
+
+    def attn():
+        return attention_keybias(q, k, v, bias, SM_SCALE)
+
+    for _ in range(args.warmup):
+        sim()
+        attn()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
+
+    ev = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        sim()
+        e[1].record()
+        attn()
+        e[2].record()
+        ev.append(e)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed / args.steps * 1e3
+    sim_ms = statistics.median(e[0].elapsed_time(e[1]) for e in ev)
+    attn_ms = statistics.median(e[1].elapsed_time(e[2]) for e in ev)
+    value = (f_sim + f_attn) / (ms_step * 1e-3) / 1e12
+    log(f"[bench] step {ms_step:.3f} ms: sim {sim_ms:.3f} ms, attn {attn_ms:.3f} ms")
+
+    kernels = {"sim_argmax_75000x25000x128": kernel_entry(f_sim, sim_ms),
+               "attn_keybias_16h_274800x68700": kernel_entry(f_attn, attn_ms)}
+
+    if not args.no_200f:
+        # Reference defaults at 200 frames x 1374 tokens: 207,955 source and
+        # 66,845 destination tokens; merged keys 66,845 (aggressive blocks) and
+        # 219,840 (core blocks, 80% kept).
+        del src, dst
+        s2, d2 = W.sim_inputs(m=207_955, n=66_845, seed=1, device=dev)
+        fn = lambda: fused_similarity_argmax(s2, d2)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 5))
+        kernels["sim_argmax_200f_207955x66845x128"] = kernel_entry(W.sim_flops(1, 207_955, 66_845, 128), t)
+        del s2, d2
+        for nk, tag in ((66_845, "aggressive"), (219_840, "core")):
+            q2, k2, v2, b2 = W.attn_inputs(m=274_800, n=nk, seed=2, device=dev)
+            fn = lambda: attention_keybias(q2, k2, v2, b2, SM_SCALE)  # noqa: E731
+            fn()
+            t = statistics.median(event_ms(fn, 3))
+            kernels[f"attn_keybias_200f_{tag}_16h_274800x{nk}"] = kernel_entry(
+                W.attn_flops(16, 274_800, nk, 64), t)
+            del q2, k2, v2, b2
+        log("[bench] 200-frame shapes done")
+
+    achieved = f_attn / (attn_ms * 1e-3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic, "kernel": "attn_keybias_kernel",
+                "flops_per_launch": f_attn}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline ...")
+        src_c, dst_c = W.sim_inputs(m=75_000, n=25_000, seed=0, device=dev)
+        cpu = cpu_baseline(src_c, dst_c, q, k, v, bias, args.cpu_budget)
+        log(f"[bench] CPU baseline {cpu['value']} TFLOP/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "ms + TFLOP/s (% bf16 MFMA peak) for sim-argmax and biased attn, 200 frames",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": ("sim-argmax [75000x128]x[25000x128] + biased attention 16 heads "
+                                "x 274800 queries x 68700 merged keys x d64 (200 frames x 1374 tokens)"),
+                   "sm_scale": SM_SCALE, "bias": "log(count), bf16, [1,16,1,N]"},
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,45 @@
+// Shared device helpers for the gfx950 kernels: vector types, the MFMA
+// wrapper, and the thread-local error channel of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gpa_mi355x.h"
+
+namespace gpa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// D = A(32x16) * B(16x32) + C, bf16 operands, fp32 accumulate.
+// Operand layout (wave64): lane l supplies A[l%32][8*(l/32) .. +8] and
+// B[8*(l/32) .. +8][l%32].  Result: lane l holds column l%32, register r
+// holds row 8*(r/4) + 4*(l/32) + (r%4).
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32x32 MFMA result held by register r of a lane in half `hi`.
+__device__ __forceinline__ constexpr int mfma_row(int r, int hi) {
+  return 8 * (r >> 2) + 4 * hi + (r & 3);
+}
+
+// D = A(16x32) * B(32x16) + C, bf16 operands, fp32 accumulate.
+// Operand layout (wave64): lane l supplies A[l%16][8*(l/16) .. +8] and
+// B[8*(l/16) .. +8][l%16].  Result: lane l holds column l%16, register r
+// holds row 4*(l/16) + r.
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace gpa
+
+// Error channel (defined in abi.hip).
+void gpa_set_error(const char* fmt, ...);
+void gpa_clear_error();

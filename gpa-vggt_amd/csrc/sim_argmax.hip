@@ -1,0 +1,405 @@
+// Fused similarity row max / argmax for gfx950 (CDNA4).
+//
+// Computes, for every source row m of a[B, M, D] against every destination
+// row n of b[B, N, D]:
+//     out_max[m] = max_n <a_m, b_n>        (bf16 inputs, fp32 accumulate)
+//     out_idx[m] = lowest n attaining it
+// without materialising the M x N score matrix.  Semantics follow the
+// reference Triton kernel merging/fused_similarity.py:33-78 (fp32 scores,
+// strict `>` across tiles at :73, first index inside a tile via tl.argmax).
+//
+// Work decomposition
+//   * A workgroup owns 256 source rows (4 waves x 4 blocks of 16; 128 rows
+//     above D=128) and one contiguous destination range ("split").  Source
+//     rows stay in VGPRs as MFMA B-operands for the whole kernel; destination
+//     rows stream through LDS in double-buffered stages of 64 rows.
+//   * Each 16x16 score tile is S^T = Dst(16xD) . Src^T(Dx16) on
+//     v_mfma_f32_16x16x32_bf16, so a lane holds one source row against 4
+//     destination rows and the running max/argmax is lane-local: one
+//     compare and two selects per score, no cross-lane traffic until the
+//     very end.  (The 16x16 shape keeps 16 tracking slots per source row,
+//     half of what the 32x32 shape needs, at the same MFMA rate.)
+//   * Splits are mapped onto XCDs (workgroup id mod 8 selects the XCD), so
+//     all workgroups on one XCD read the same destination range and that
+//     range stays resident in the XCD's L2.  Partial (max, idx) pairs per
+//     split are merged by a second tiny kernel with the same tie rule.
+#include "gpa_common.h"
+
+#include <math.h>
+
+namespace gpa {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kTN = 64;  // destination rows per LDS stage
+
+// 16-row source blocks held per wave (ks = D/32): four up to D=128, two
+// above, which keeps the kernel within the VGPR budget of two waves/SIMD.
+__host__ __device__ constexpr int src_blocks(int ks) { return ks <= 4 ? 4 : 2; }
+__host__ __device__ constexpr int rows_per_wg(int ks) { return kWaves * src_blocks(ks) * 16; }
+
+struct SimArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  float* out_max;      // final outputs (splits == 1)
+  int64_t* out_idx;
+  float* part_max;     // [B][splits][M] partials (splits > 1)
+  int32_t* part_idx;
+  int64_t M, N;
+  int64_t a_sb, a_sm, b_sb, b_sn, omax_sb, oidx_sb;
+  int splits;          // destination splits (1, 2, 4, 8 or a multiple of 8)
+  int mblocks;         // source row blocks, padded to the mapping granularity
+  int64_t n_chunk;     // destination rows per split (multiple of kTN)
+};
+
+// Workgroup id -> (source block, split).  Workgroups are dispatched to the
+// eight XCDs round-robin, so `bid & 7` is the XCD; every XCD is given whole
+// splits so that its L2 only ever holds one destination range.
+__device__ __forceinline__ void map_block(const SimArgs& p, int bid, int& mblock, int& split) {
+  if (p.splits == 1) {
+    mblock = bid;
+    split = 0;
+    return;
+  }
+  const int x = bid & 7, y = bid >> 3;
+  if (p.splits <= 8) {
+    const int g = 8 / p.splits;  // XCDs sharing one split
+    split = x / g;
+    mblock = y * g + (x % g);
+  } else {
+    const int k = p.splits / 8;  // splits per XCD
+    split = x * k + (y % k);
+    mblock = y / k;
+  }
+}
+
+template <int KS>
+__global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
+  constexpr int kSB = src_blocks(KS);
+  constexpr int kRowsPerWG = rows_per_wg(KS);
+  constexpr int D = KS * 32;
+  constexpr int NCH = D / 8;  // 16-byte chunks per row
+  // XOR swizzle of the chunk index by the row, kept inside the row: the mask
+  // is the largest power of two (<= 16) dividing the chunk count.
+  constexpr int SWZ = ((NCH & -NCH) >= 16 ? 16 : (NCH & -NCH)) - 1;
+  constexpr int ROW_BYTES = D * 2;
+  constexpr int STAGE_BYTES = kTN * ROW_BYTES;
+  constexpr int LOADS = kTN * NCH / 256;  // chunks per thread per stage
+  static_assert(LOADS * 256 == kTN * NCH, "stage must split evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int quad = lane >> 4, l16 = lane & 15;
+  const int64_t batch = blockIdx.y;
+  int mblock, split;
+  map_block(p, blockIdx.x, mblock, split);
+  const int64_t m_wg = (int64_t)mblock * kRowsPerWG;
+  if (m_wg >= p.M) return;  // padding block: the whole workgroup leaves together
+
+  const int64_t n_begin = (int64_t)split * p.n_chunk;
+  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
+  const uint16_t* A = p.a + batch * p.a_sb;
+  const uint16_t* Bm = p.b + batch * p.b_sb;
+
+  // Source rows as MFMA B-operands: lane supplies row (lane%16) of its block,
+  // features 8*quad .. +8 of each 32-wide k-step.
+  bf16x8 sf[kSB][KS];
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb) {
+    const int64_t row = m_wg + wave * (kSB * 16) + sb * 16 + l16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (row < p.M) {
+        sf[sb][ks] = *reinterpret_cast<const bf16x8*>(A + row * p.a_sm + ks * 32 + quad * 8);
+      } else {
+        sf[sb][ks] = bf16x8{};
+      }
+    }
+  }
+
+  // Lane-local running state: per accumulator slot, the best score and the
+  // 16-row tile that first reached it.
+  float best[kSB][4];
+  int bt[kSB][4];
+  const int tile0 = (int)(n_begin >> 4);
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      best[sb][r] = -INFINITY;
+      bt[sb][r] = tile0;
+    }
+
+  const int nstages = n_end > n_begin ? (int)((n_end - n_begin + kTN - 1) / kTN) : 0;
+  u32x4 stage[LOADS];
+
+  auto load_stage = [&](int st) {
+    const int64_t base = n_begin + (int64_t)st * kTN;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int id = j * 256 + tid;
+      const int row = id / NCH, ch = id % NCH;
+      const int64_t n = base + row;
+      stage[j] = n < n_end ? *reinterpret_cast<const u32x4*>(Bm + n * p.b_sn + ch * 8) : u32x4{};
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int id = j * 256 + tid;
+      const int row = id / NCH, ch = id % NCH;
+      *reinterpret_cast<u32x4*>(lds + buf * STAGE_BYTES + row * ROW_BYTES +
+                                ((ch ^ (row & SWZ)) << 4)) = stage[j];
+    }
+  };
+
+  if (nstages > 0) {
+    load_stage(0);
+    store_stage(0);
+  }
+  __syncthreads();
+
+  for (int st = 0; st < nstages; ++st) {
+    const int cur = st & 1;
+    if (st + 1 < nstages) load_stage(st + 1);
+    const int64_t base = n_begin + (int64_t)st * kTN;
+    const uint8_t* L = lds + cur * STAGE_BYTES;
+#pragma unroll
+    for (int u = 0; u < kTN / 16; ++u) {
+      const int64_t tile_n = base + u * 16;
+      if (tile_n >= n_end) break;
+      f32x4 acc[kSB];
+#pragma unroll
+      for (int sb = 0; sb < kSB; ++sb) acc[sb] = f32x4{};
+      const int row = u * 16 + l16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int ch = 4 * ks + quad;
+        const bf16x8 af =
+            *reinterpret_cast<const bf16x8*>(L + row * ROW_BYTES + ((ch ^ (row & SWZ)) << 4));
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32(af, sf[sb][ks], acc[sb]);
+      }
+      const int tile = (int)(tile_n >> 4);
+      if (tile_n + 16 <= n_end) {
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float v = acc[sb][r];
+            const bool upd = v > best[sb][r];
+            best[sb][r] = upd ? v : best[sb][r];
+            bt[sb][r] = upd ? tile : bt[sb][r];
+          }
+      } else {
+#pragma unroll
+        for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float v = acc[sb][r];
+            const bool upd = (tile_n + 4 * quad + r < n_end) && v > best[sb][r];
+            best[sb][r] = upd ? v : best[sb][r];
+            bt[sb][r] = upd ? tile : bt[sb][r];
+          }
+      }
+    }
+    if (st + 1 < nstages) store_stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Reduce the 4 slots of each lane, then the four lanes (quads) that share a
+  // source row: highest score wins, ties go to the lowest destination index.
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = best[sb][r];
+      const int idx = bt[sb][r] * 16 + 4 * quad + r;
+      const bool take = v > bv || (v == bv && idx < bi);
+      bv = take ? v : bv;
+      bi = take ? idx : bi;
+    }
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float ov = __shfl_xor(bv, sh);
+      const int oi = __shfl_xor(bi, sh);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    const int64_t m = m_wg + wave * (kSB * 16) + sb * 16 + l16;
+    if (quad == 0 && m < p.M) {
+      if (p.splits == 1) {
+        p.out_max[batch * p.omax_sb + m] = bv;
+        p.out_idx[batch * p.oidx_sb + m] = bi;
+      } else {
+        const int64_t o = (batch * p.splits + split) * p.M + m;
+        p.part_max[o] = bv;
+        p.part_idx[o] = bi;
+      }
+    }
+  }
+}
+
+// Merge per-split partials in split order; strict `>` keeps the earlier
+// split (lower destination indices) on ties.
+__global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_t B) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= B * p.M) return;
+  const int64_t batch = t / p.M, m = t % p.M;
+  const int64_t base = batch * p.splits * p.M + m;
+  float bv = p.part_max[base];
+  int bi = p.part_idx[base];
+  for (int s = 1; s < p.splits; ++s) {
+    const float v = p.part_max[base + s * p.M];
+    if (v > bv) {
+      bv = v;
+      bi = p.part_idx[base + s * p.M];
+    }
+  }
+  p.out_max[batch * p.omax_sb + m] = bv;
+  p.out_idx[batch * p.oidx_sb + m] = bi;
+}
+
+struct SimPlan {
+  int splits;
+  int mblocks;       // padded source blocks
+  int64_t n_chunk;
+  size_t ws_bytes;
+};
+
+SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
+  SimPlan pl{};
+  const int rows = rows_per_wg((int)(D / 32));
+  const int64_t mb = (M + rows - 1) / rows;
+  // Split the destination range until the grid holds >= 2048 workgroups
+  // (8 per CU on 256 CUs) or a split would drop below 512 rows.  Once there
+  // are several splits, use at least 8 so that each XCD owns one range.
+  int splits = 1;
+  while (splits < 16 && mb * B * splits < 2048 && N / (splits * 2) >= 512) splits *= 2;
+  if (splits > 1 && splits < 8 && N / 8 >= 512) splits = 8;
+  pl.splits = splits;
+  int64_t mbp = mb;
+  if (splits > 1 && splits < 8) {
+    const int g = 8 / splits;
+    mbp = (mb + g - 1) / g * g;
+  }
+  pl.mblocks = (int)mbp;
+  const int64_t per = (N + splits - 1) / splits;
+  pl.n_chunk = (per + kTN - 1) / kTN * kTN;
+  pl.ws_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
+  return pl;
+}
+
+}  // namespace
+}  // namespace gpa
+
+using namespace gpa;
+
+extern "C" size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D) {
+  if (B <= 0 || M <= 0 || N <= 0) return 0;
+  return make_plan(B, M, N, D).ws_bytes;
+}
+
+extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max, int64_t* out_idx,
+                                   int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
+                                   int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
+                                   int64_t oidx_sb, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  gpa_clear_error();
+  if (B < 0 || M < 0 || N < 0 || D < 0) {
+    gpa_set_error("gpa_sim_argmax_bf16: negative size (B=%lld M=%lld N=%lld D=%lld)",
+                  (long long)B, (long long)M, (long long)N, (long long)D);
+    return GPA_E_INVALID;
+  }
+  if (B == 0 || M == 0) return GPA_OK;
+  if (N == 0) {
+    gpa_set_error("gpa_sim_argmax_bf16: empty destination set (N=0)");
+    return GPA_E_INVALID;
+  }
+  if (!a || !b || !out_max || !out_idx) {
+    gpa_set_error("gpa_sim_argmax_bf16: null tensor pointer");
+    return GPA_E_INVALID;
+  }
+  if (D % 32 != 0 || D < 32 || D > 256) {
+    gpa_set_error("gpa_sim_argmax_bf16: feature dim D=%lld unsupported (multiple of 32, 32..256)",
+                  (long long)D);
+    return GPA_E_UNSUPPORTED;
+  }
+  if (N > (int64_t)0x7fffff00 || M > ((int64_t)1 << 40)) {
+    gpa_set_error("gpa_sim_argmax_bf16: N=%lld exceeds the int32 index range", (long long)N);
+    return GPA_E_UNSUPPORTED;
+  }
+  const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+  if ((pa % 16) || (pb % 16) || (a_sm % 8) || (b_sn % 8) || (a_sb % 8) || (b_sb % 8) ||
+      a_sm < D || b_sn < D) {
+    gpa_set_error("gpa_sim_argmax_bf16: rows must be 16-byte aligned with unit feature stride "
+                  "(a_sm=%lld b_sn=%lld a_sb=%lld b_sb=%lld)",
+                  (long long)a_sm, (long long)b_sn, (long long)a_sb, (long long)b_sb);
+    return GPA_E_INVALID;
+  }
+  if (B > 65535) {
+    gpa_set_error("gpa_sim_argmax_bf16: batch %lld exceeds the grid limit", (long long)B);
+    return GPA_E_UNSUPPORTED;
+  }
+
+  const SimPlan pl = make_plan(B, M, N, D);
+  SimArgs p{};
+  p.a = (const uint16_t*)a;
+  p.b = (const uint16_t*)b;
+  p.out_max = out_max;
+  p.out_idx = out_idx;
+  p.M = M;
+  p.N = N;
+  p.a_sb = a_sb;
+  p.a_sm = a_sm;
+  p.b_sb = b_sb;
+  p.b_sn = b_sn;
+  p.omax_sb = omax_sb;
+  p.oidx_sb = oidx_sb;
+  p.splits = pl.splits;
+  p.mblocks = pl.mblocks;
+  p.n_chunk = pl.n_chunk;
+  if (pl.splits > 1) {
+    if (!workspace || workspace_bytes < pl.ws_bytes) {
+      gpa_set_error("gpa_sim_argmax_bf16: workspace of %zu bytes required, %zu given",
+                    pl.ws_bytes, workspace ? workspace_bytes : (size_t)0);
+      return GPA_E_WORKSPACE;
+    }
+    p.part_max = (float*)workspace;
+    p.part_idx = (int32_t*)((char*)workspace + (size_t)(B * pl.splits * M) * sizeof(float));
+  }
+  const int64_t grid_x = (int64_t)pl.mblocks * pl.splits;
+  if (grid_x > 0x7fffffff) {
+    gpa_set_error("gpa_sim_argmax_bf16: grid too large");
+    return GPA_E_UNSUPPORTED;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)grid_x, (unsigned)B), block(256);
+  switch (D / 32) {
+#define GPA_SIM_CASE(ks) \
+  case ks: hipLaunchKernelGGL(sim_argmax_kernel<ks>, grid, block, 0, s, p); break;
+    GPA_SIM_CASE(1) GPA_SIM_CASE(2) GPA_SIM_CASE(3) GPA_SIM_CASE(4)
+    GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
+#undef GPA_SIM_CASE
+    default:
+      gpa_set_error("gpa_sim_argmax_bf16: D=%lld has no kernel instance", (long long)D);
+      return GPA_E_UNSUPPORTED;
+  }
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && pl.splits > 1) {
+    const int64_t total = B * M;
+    hipLaunchKernelGGL(sim_argmax_merge_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, s, p, B);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) {
+    gpa_set_error("gpa_sim_argmax_bf16: launch failed: %s", hipGetErrorString(e));
+    return GPA_E_LAUNCH;
+  }
+  return GPA_OK;
+}

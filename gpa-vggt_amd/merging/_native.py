@@ -1,0 +1,251 @@
+"""Loader for the gfx950 shared library and the PyTorch custom ops over it.
+
+The library (`_lib/libgpa_mi355x.so`, built by `gpa-vggt_amd/build.py`)
+exports the plain C ABI declared in `include/gpa_mi355x.h`.  This module
+binds it with ctypes *after* importing torch, so the library resolves
+`libamdhip64.so.7` to the HIP runtime torch already loaded, and registers
+two custom ops:
+
+    gpa::sim_argmax(Tensor a, Tensor b) -> (Tensor max_f32, Tensor idx_i64)
+    gpa::attn_keybias(Tensor q, Tensor k, Tensor v, Tensor? bias,
+                      float sm_scale, bool return_lse) -> (Tensor o, Tensor lse)
+
+Both launch on torch's current stream of the input's device.  There is no
+fallback: a missing library or a non-GPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional, Tuple
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
+ABI_VERSION = 1
+
+GPA_OK = 0
+GPA_E_INVALID = -1
+GPA_E_UNSUPPORTED = -2
+GPA_E_WORKSPACE = -3
+GPA_E_LAUNCH = -4
+
+GPA_BIAS_NONE = 0
+GPA_BIAS_F32 = 1
+GPA_BIAS_BF16 = 2
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+
+class NativeLibraryError(RuntimeError):
+    """The gfx950 library is missing, stale or failed to load."""
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    lib.gpa_abi_version.restype = ctypes.c_int
+    lib.gpa_abi_version.argtypes = []
+    lib.gpa_last_error.restype = ctypes.c_char_p
+    lib.gpa_last_error.argtypes = []
+    lib.gpa_sim_argmax_workspace_bytes.restype = ctypes.c_size_t
+    lib.gpa_sim_argmax_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
+    lib.gpa_sim_argmax_bf16.restype = ctypes.c_int
+    lib.gpa_sim_argmax_bf16.argtypes = [
+        _vp, _vp, _vp, _vp,            # a, b, out_max, out_idx
+        _i64, _i64, _i64, _i64,        # B, M, N, D
+        _i64, _i64, _i64, _i64,        # a_sb, a_sm, b_sb, b_sn
+        _i64, _i64,                    # omax_sb, oidx_sb
+        _vp, ctypes.c_size_t, _vp,     # workspace, workspace_bytes, stream
+    ]
+    lib.gpa_attn_keybias_bf16.restype = ctypes.c_int
+    lib.gpa_attn_keybias_bf16.argtypes = [
+        _vp, _vp, _vp,                 # q, k, v
+        _vp, ctypes.c_int,             # bias, bias_kind
+        _i64, _i64, _i64,              # bias strides (b, h, n)
+        _vp, _vp,                      # o, lse
+        _i64, _i64, _i64, _i64, _i64,  # B, H, M, N, D
+        _i64, _i64, _i64,              # q strides
+        _i64, _i64, _i64,              # k strides
+        _i64, _i64, _i64,              # v strides
+        _i64, _i64, _i64,              # o strides
+        _i64, _i64,                    # lse strides
+        ctypes.c_float, _vp,           # sm_scale, stream
+    ]
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded on first use)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryError(
+                    f"{LIB_PATH} is not built; run `python gpa-vggt_amd/build.py` "
+                    "(hipcc, gfx950) before using the merging ops")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            _bind(handle)
+            ver = handle.gpa_abi_version()
+            if ver != ABI_VERSION:
+                raise NativeLibraryError(
+                    f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+            _lib = handle
+    return _lib
+
+
+def exported_symbols() -> Tuple[str, ...]:
+    return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
+            "gpa_sim_argmax_bf16", "gpa_attn_keybias_bf16")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == GPA_OK:
+        return
+    msg = (lib().gpa_last_error() or b"").decode(errors="replace")
+    if rc in (GPA_E_INVALID, GPA_E_WORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    if rc == GPA_E_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError("the gfx950 merging kernels need GPU tensors, got device "
+                             f"{t.device}")
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _rows_ok(t: torch.Tensor, align_elems: int) -> bool:
+    """Unit inner stride, other strides multiples of `align_elems`, aligned base."""
+    if t.stride(-1) != 1:
+        return False
+    if t.data_ptr() % (2 * align_elems) != 0:
+        return False
+    return all(s % align_elems == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+
+
+# --------------------------------------------------------------------------
+# gpa::sim_argmax
+# --------------------------------------------------------------------------
+
+@torch.library.custom_op("gpa::sim_argmax", mutates_args=())
+def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Row max (fp32) and lowest-index argmax (int64) of a @ b^T, bf16 inputs."""
+    dev = _require_gpu(a, b)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise ValueError(f"gpa::sim_argmax takes bf16 inputs, got {a.dtype}/{b.dtype}")
+    if a.dim() != 3 or b.dim() != 3 or a.shape[0] != b.shape[0] or a.shape[2] != b.shape[2]:
+        raise ValueError(f"gpa::sim_argmax shape mismatch: a {tuple(a.shape)}, b {tuple(b.shape)}")
+    if not _rows_ok(a, 8):
+        a = a.contiguous()
+    if not _rows_ok(b, 8):
+        b = b.contiguous()
+    B, M, D = a.shape
+    N = b.shape[1]
+    out_max = torch.empty(B, M, device=dev, dtype=torch.float32)
+    out_idx = torch.empty(B, M, device=dev, dtype=torch.int64)
+    if B == 0 or M == 0:
+        return out_max, out_idx
+    L = lib()
+    ws_bytes = L.gpa_sim_argmax_workspace_bytes(B, M, N, D)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    with torch.cuda.device(dev):
+        rc = L.gpa_sim_argmax_bf16(
+            a.data_ptr(), b.data_ptr(), out_max.data_ptr(), out_idx.data_ptr(),
+            B, M, N, D, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+            out_max.stride(0), out_idx.stride(0),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+    _check(rc, "gpa::sim_argmax")
+    return out_max, out_idx
+
+
+@sim_argmax.register_fake
+def _sim_argmax_fake(a, b):
+    B, M, _ = a.shape
+    return a.new_empty(B, M, dtype=torch.float32), a.new_empty(B, M, dtype=torch.int64)
+
+
+# --------------------------------------------------------------------------
+# gpa::attn_keybias
+# --------------------------------------------------------------------------
+
+@torch.library.custom_op("gpa::attn_keybias", mutates_args=())
+def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                 bias: Optional[torch.Tensor], sm_scale: float,
+                 return_lse: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """softmax(q k^T * sm_scale + bias) v with bf16 q/k/v and a per-key bias.
+
+    q [B,H,M,64], k/v [B,H,N,64] bf16; bias broadcastable to [B,H,1,N]
+    (fp32 or bf16) or None.  Returns o [B,H,M,64] bf16 and, if return_lse,
+    the log2 log-sum-exp [B,H,M] fp32 (else an empty tensor).
+    """
+    tensors = [q, k, v] + ([bias] if bias is not None else [])
+    dev = _require_gpu(*tensors)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"gpa::attn_keybias takes bf16 {name}, got {t.dtype}")
+        if t.dim() != 4:
+            raise ValueError(f"gpa::attn_keybias: {name} must be [B,H,T,D], got {tuple(t.shape)}")
+    B, H, M, D = q.shape
+    N = k.shape[2]
+    if k.shape != (B, H, N, D) or v.shape != (B, H, N, D):
+        raise ValueError(f"gpa::attn_keybias shape mismatch: q {tuple(q.shape)}, "
+                         f"k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if not _rows_ok(q, 8):
+        q = q.contiguous()
+    if not _rows_ok(k, 8):
+        k = k.contiguous()
+    if not _rows_ok(v, 4):
+        v = v.contiguous()
+    bias_kind, bias_ptr, bsb, bsh, bsn = GPA_BIAS_NONE, None, 0, 0, 0
+    if bias is not None:
+        if bias.dtype not in (torch.float32, torch.bfloat16):
+            bias = bias.float()
+        try:
+            bx = bias.expand(B, H, 1, N)
+        except RuntimeError as exc:
+            raise ValueError(f"gpa::attn_keybias: bias {tuple(bias.shape)} does not broadcast to "
+                             f"[B,H,1,N]=[{B},{H},1,{N}]") from exc
+        bias_kind = GPA_BIAS_F32 if bx.dtype == torch.float32 else GPA_BIAS_BF16
+        bias_ptr = bx.data_ptr()
+        bsb, bsh, bsn = bx.stride(0), bx.stride(1), bx.stride(3)
+    o = torch.empty(B, H, M, D, device=dev, dtype=torch.bfloat16)
+    lse = (torch.empty(B, H, M, device=dev, dtype=torch.float32) if return_lse
+           else torch.empty(0, device=dev, dtype=torch.float32))
+    if B == 0 or H == 0 or M == 0:
+        return o, lse
+    with torch.cuda.device(dev):
+        rc = lib().gpa_attn_keybias_bf16(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), bias_ptr, bias_kind, bsb, bsh, bsn,
+            o.data_ptr(), lse.data_ptr() if return_lse else None,
+            B, H, M, N, D,
+            q.stride(0), q.stride(1), q.stride(2),
+            k.stride(0), k.stride(1), k.stride(2),
+            v.stride(0), v.stride(1), v.stride(2),
+            o.stride(0), o.stride(1), o.stride(2),
+            lse.stride(0) if return_lse else 0, lse.stride(1) if return_lse else 0,
+            float(sm_scale), _stream(dev))
+    _check(rc, "gpa::attn_keybias")
+    return o, lse
+
+
+@attn_keybias.register_fake
+def _attn_keybias_fake(q, k, v, bias, sm_scale, return_lse):
+    B, H, M, D = q.shape
+    o = q.new_empty(B, H, M, D, dtype=torch.bfloat16)
+    lse = q.new_empty((B, H, M) if return_lse else (0,), dtype=torch.float32)
+    return o, lse

@@ -1,0 +1,60 @@
+"""Fused similarity + argmax for bipartite token matching, on gfx950.
+
+Drop-in for the reference's `merging/fused_similarity.py`: same function
+name, arguments, dtype contract and return types
+(`fused_similarity_argmax`, reference :81-112).  The kernel itself is the
+hand-written HIP kernel `sim_argmax_kernel` in `csrc/sim_argmax.hip`,
+reached through the `gpa::sim_argmax` custom op.
+
+Numerics: fp32 accumulation of bf16 products; the max is taken over the fp32
+scores (not bf16-rounded scores as in the chunked torch path), and ties
+resolve to the lowest destination index, as the reference kernel's strict
+`>` across tiles plus `tl.argmax`'s first index do
+(merging/fused_similarity.py:71-75).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _native
+
+__all__ = ["fused_similarity_argmax"]
+
+_MAX_D = 256
+
+
+def fused_similarity_argmax(a: torch.Tensor, b: torch.Tensor):
+    """node_max, node_idx = (a @ b.transpose(-1,-2)).max(dim=-1), fused.
+
+    a: [B, M, D] src metric, b: [B, N, D] dst metric (GPU, bf16 or fp32).
+    Returns node_max [B, M] (a.dtype) and node_idx [B, M] (int64).
+    Follows merging/fused_similarity.py:81-112: fp32 inputs are rounded to
+    bf16 first (:90-95), the max comes back in the input dtype (:112).
+    """
+    if not (a.is_cuda and b.is_cuda and a.dim() == 3 and b.dim() == 3):
+        raise AssertionError(
+            "fused_similarity_argmax expects 3-D GPU tensors "
+            f"(got a {tuple(a.shape)} on {a.device}, b {tuple(b.shape)} on {b.device})")
+    out_dtype = a.dtype
+    if a.dtype == torch.float16 or b.dtype == torch.float16:
+        raise NotImplementedError("fused_similarity_argmax: fp16 inputs are not supported; "
+                                  "the gfx950 kernel runs bf16 (pass bf16 or fp32)")
+    if a.dtype == torch.float32:
+        a = a.to(torch.bfloat16)
+    if b.dtype == torch.float32:
+        b = b.to(torch.bfloat16)
+    D = a.shape[-1]
+    if b.shape[-1] != D:
+        raise ValueError(f"feature dims differ: {D} vs {b.shape[-1]}")
+    if D > _MAX_D:
+        raise NotImplementedError(
+            f"fused_similarity_argmax: feature dim {D} > {_MAX_D} is not implemented on gfx950 "
+            "(use a metric projection, metric_dim <= 256)")
+    if D % 32:
+        # Zero features add nothing to any dot product, so padding is exact.
+        pad = 32 - D % 32
+        a = F.pad(a, (0, pad))
+        b = F.pad(b, (0, pad))
+    node_max, node_idx = torch.ops.gpa.sim_argmax(a, b)
+    return node_max.to(out_dtype), node_idx

@@ -1,0 +1,186 @@
+"""Bipartite K/V token merge for GPA-VGGT, on gfx950.
+
+Drop-in for the reference's `merging/merge.py`: `token_merge_bipartite2d`
+keeps its signature and returns the same closure (`merge(x, mode)`,
+`merge.heads(t, mode)`, `merge.size`), and `PROJ_SEED` keeps its value.
+The similarity step always runs the gfx950 kernel (`fused_similarity_argmax`);
+there is no chunked-bmm fallback.
+
+Orderings the reference leaves to torch's sort are fixed here:
+  * dst / src order (reference :165): tokens in increasing position within
+    each class -- a stable sort of the -1/0 mask;
+  * merge order (reference :199): descending node_max, ties by increasing
+    source position -- a stable descending sort.
+These are the orders torch's GPU radix sort produces for such inputs.
+`merge.index` exposes the index tensors for inspection.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+from typing import Callable, Optional
+
+import torch
+
+from .fused_similarity import fused_similarity_argmax
+
+__all__ = ["token_merge_bipartite2d", "PROJ_SEED", "dst_mask", "num_dst_tokens"]
+
+# Seed of the fixed Gaussian basis used by the metric_dim random projection
+# (reference merging/merge.py:10).
+PROJ_SEED = 1234
+
+
+def num_dst_tokens(num_imgs: int, w: int, h: int, sx: int, sy: int, num_special: int,
+                   no_rand: bool) -> int:
+    """Destination count implied by the mask rules of `dst_mask` (closed form)."""
+    tpi = w * h + num_special
+    if num_imgs <= 0:
+        return 0
+    if num_imgs == 1:
+        return tpi
+    per_frame = num_special + (0 if no_rand else (h // sy) * (w // sx))
+    return tpi + (num_imgs - 1) * per_frame
+
+
+def dst_mask(num_imgs: int, w: int, h: int, sx: int, sy: int, num_special: int,
+             no_rand: bool, generator: Optional[torch.Generator],
+             device: torch.device) -> torch.Tensor:
+    """[num_imgs * (w*h + num_special)] int64 mask: -1 = dst, 0 = src.
+
+    Rules of merging/merge.py:85-163: every token of frame 0 and the special
+    tokens of every frame are dst; for frames >= 1 one cell of each sy x sx
+    window is dst, drawn with one `torch.randint(sy*sx, (frames-1, h//sy,
+    w//sx), generator=...)` call.  As in the reference, the window grid is
+    laid out with row length (w//sx)*sx over the first (h//sy)*sy*(w//sx)*sx
+    patch positions of the frame; `no_rand=True` marks no patch of frames
+    >= 1 (reference :105-118 writes an all-zero pattern).
+    """
+    tpi = w * h + num_special
+    n = num_imgs * tpi
+    mask = torch.zeros(n, device=device, dtype=torch.int64)
+    if num_imgs <= 0:
+        return mask
+    mask[:tpi] = -1
+    if num_imgs == 1:
+        return mask
+    starts = torch.arange(1, num_imgs, device=device) * tpi
+    mask[(starts[:, None] + torch.arange(num_special, device=device)).reshape(-1)] = -1
+    if no_rand:
+        return mask
+    hsy, wsx = h // sy, w // sx
+    cell = torch.randint(sy * sx, size=(num_imgs - 1, hsy, wsx), device=device,
+                         generator=generator)
+    row_len = wsx * sx
+    ys = torch.arange(hsy, device=device).view(1, hsy, 1) * sy + cell // sx
+    xs = torch.arange(wsx, device=device).view(1, 1, wsx) * sx + cell % sx
+    pos = starts.view(-1, 1, 1) + num_special + ys * row_len + xs
+    mask[pos.reshape(-1)] = -1
+    return mask
+
+
+def token_merge_bipartite2d(
+    metric: torch.Tensor,
+    w: int,
+    h: int,
+    sx: int,
+    sy: int,
+    r: int,
+    no_rand: bool = False,
+    generator: Optional[torch.Generator] = None,
+    metric_dim: int = 0,
+    num_special: int = 5,
+) -> Callable:
+    """Bipartite token merging over the multi-frame token sequence.
+
+    Same contract as merging/merge.py:39-256.  Tokens are split into dst (one
+    random token per (sx, sy) window, every token of the first frame, every
+    special token) and src; the r src tokens most similar to a dst token are
+    merged into it.
+
+    Returns merge(x [B, N, C], mode) -> [B, N - r, C] laid out as
+    [unmerged src | dst]; merge.heads(t [B, H, N, D], mode) merges in
+    head-major layout; merge.size [B, N - r] (B == 1, else None) holds the
+    number of tokens behind each output slot.
+    """
+    B, N, C = metric.shape
+    if r <= 0:
+        raise ValueError("token_merge_bipartite2d: r must be positive")
+    tpi = w * h + num_special
+    num_imgs = N // tpi
+    if tpi * num_imgs != N:
+        raise AssertionError(
+            f"Token count doesn't match (w*h+{num_special})*num_imgs: N={N} w={w} h={h}")
+    if not metric.is_cuda:
+        raise ValueError("token_merge_bipartite2d runs on the GPU; got a tensor on "
+                         f"{metric.device}")
+    dev = metric.device
+
+    with torch.no_grad():
+        mask = dst_mask(num_imgs, w, h, sx, sy, num_special, no_rand, generator, dev)
+        num_dst = num_dst_tokens(num_imgs, w, h, sx, sy, num_special, no_rand)
+        order = torch.argsort(mask, stable=True)  # dst positions first, then src
+        b_pos = order[:num_dst]
+        a_pos = order[num_dst:]
+        num_src = N - num_dst
+
+        if metric_dim and metric_dim < C:
+            g_proj = torch.Generator(device=dev)
+            g_proj.manual_seed(PROJ_SEED)
+            proj = torch.randn(C, metric_dim, device=dev, dtype=torch.float32,
+                               generator=g_proj).to(metric.dtype)
+            metric = metric @ proj
+        metric = metric / metric.norm(dim=-1, keepdim=True)
+        a = metric.index_select(1, a_pos)
+        b = metric.index_select(1, b_pos)
+
+        r = min(num_src, r)
+        if num_src > 0:
+            node_max, node_idx = fused_similarity_argmax(a, b)
+        else:
+            node_max = metric.new_empty(B, 0)
+            node_idx = torch.empty(B, 0, device=dev, dtype=torch.int64)
+        edge = torch.argsort(node_max, dim=-1, descending=True, stable=True)
+        src_rank = edge[:, :r]          # merged source rows (rows of `a`)
+        unm_rank = edge[:, r:]          # kept source rows
+        dst_slot = torch.gather(node_idx, 1, src_rank)        # [B, r] dst slot per merged row
+        unm_abs = a_pos[unm_rank]                             # [B, unm_len] token positions
+        src_abs = a_pos[src_rank]                             # [B, r]
+        unm_len = unm_rank.shape[1]
+
+        size = torch.ones(B, unm_len + num_dst, device=dev, dtype=torch.float32)
+        size[:, unm_len:].scatter_add_(1, dst_slot, torch.ones(B, r, device=dev,
+                                                                dtype=torch.float32))
+
+    def merge(x: torch.Tensor, mode: str = "mean") -> torch.Tensor:
+        """[B, N, C] -> [B, unm_len + num_dst, C]: unmerged src, then dst."""
+        nb, _, c = x.shape
+        out = torch.empty(nb, unm_len + num_dst, c, device=x.device, dtype=x.dtype)
+        torch.gather(x, 1, unm_abs[..., None].expand(nb, unm_len, c), out=out[:, :unm_len])
+        torch.gather(x, 1, b_pos.view(1, -1, 1).expand(nb, num_dst, c), out=out[:, unm_len:])
+        moved = torch.gather(x, 1, src_abs[..., None].expand(nb, r, c))
+        out[:, unm_len:].scatter_reduce_(1, dst_slot[..., None].expand(nb, r, c), moved,
+                                         reduce=mode)
+        return out
+
+    def merge_heads(t: torch.Tensor, mode: str = "mean") -> torch.Tensor:
+        """Merge [B, H, N, D] K/V directly in the attention-kernel layout."""
+        nb, nh, ntok, d = t.shape
+        if nb != B or ntok != N:
+            raise ValueError("merge_heads input does not match the merge mapping")
+        out = torch.empty(nb, nh, unm_len + num_dst, d, device=t.device, dtype=t.dtype)
+        torch.gather(t, 2, unm_abs[:, None, :, None].expand(nb, nh, unm_len, d),
+                     out=out[:, :, :unm_len])
+        torch.gather(t, 2, b_pos.view(1, 1, -1, 1).expand(nb, nh, num_dst, d),
+                     out=out[:, :, unm_len:])
+        moved = torch.gather(t, 2, src_abs[:, None, :, None].expand(nb, nh, r, d))
+        out[:, :, unm_len:].scatter_reduce_(
+            2, dst_slot[:, None, :, None].expand(nb, nh, r, d), moved, reduce=mode)
+        return out
+
+    merge.size = size if B == 1 else None
+    merge.heads = merge_heads
+    merge.index = SimpleNamespace(
+        a_idx=a_pos, b_idx=b_pos, node_max=node_max, node_idx=node_idx, edge_idx=edge,
+        dst_idx=dst_slot, unm_abs_idx=unm_abs, src_abs_idx=src_abs,
+        num_dst=num_dst, num_src=num_src, r=r, unm_len=unm_len, mask=mask)
+    return merge

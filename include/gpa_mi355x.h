@@ -1,0 +1,106 @@
+/*
+ * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
+ *
+ * Two kernels sit behind this boundary:
+ *
+ *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
+ *                           source and destination token metrics
+ *                           (replaces merging/fused_similarity.py:81-112,
+ *                            the Triton `_sim_argmax_kernel` at :33-78).
+ *   gpa_attn_keybias_bf16 — flash attention with a per-key additive bias
+ *                           (replaces merging/fused_attention.py:130-180,
+ *                            the Triton `_attn_keybias_kernel` at :70-127).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are device pointers owned by the caller.  The
+ *     library allocates nothing and keeps no reference after returning.
+ *   - Element strides are in elements (not bytes).  The innermost (feature)
+ *     dimension has unit stride; row pointers must be 16-byte aligned.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
+ *     legacy default stream).  Functions return GPA_OK (0) after a successful
+ *     launch or a negative GPA_E* code; gpa_last_error() then holds a
+ *     message for the calling thread.
+ *   - The library is stateless and reentrant: tile shapes are a deterministic
+ *     function of the problem shape (no autotuning, no global caches).
+ */
+#ifndef GPA_MI355X_H
+#define GPA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GPA_ABI_VERSION 1
+
+enum {
+  GPA_OK = 0,
+  GPA_E_INVALID = -1,      /* null pointer, negative size, bad stride/alignment */
+  GPA_E_UNSUPPORTED = -2,  /* shape outside what the kernels implement */
+  GPA_E_WORKSPACE = -3,    /* workspace missing or too small */
+  GPA_E_LAUNCH = -4        /* the HIP runtime rejected the launch */
+};
+
+/* Bias element types accepted by gpa_attn_keybias_bf16. */
+enum { GPA_BIAS_NONE = 0, GPA_BIAS_F32 = 1, GPA_BIAS_BF16 = 2 };
+
+/* ABI version of the loaded library (GPA_ABI_VERSION at build time). */
+int gpa_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* gpa_last_error(void);
+
+/* Bytes of device workspace gpa_sim_argmax_bf16 needs for this shape
+ * (0 when the kernel writes its outputs directly). */
+size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D);
+
+/*
+ * Fused similarity row max / argmax.
+ *   a [B, M, D] bf16 (source metric), b [B, N, D] bf16 (destination metric)
+ *   out_max[b*omax_sb + m] = max_n  sum_d a[b,m,d] * b[b,n,d]   (fp32 accumulate)
+ *   out_idx[b*oidx_sb + m] = the lowest n attaining that maximum (int64)
+ * Replaces merging/fused_similarity.py:81-112 (`fused_similarity_argmax`);
+ * the index tie rule follows the kernel's strict `>` at
+ * merging/fused_similarity.py:73 together with tl.argmax's first index.
+ * D must be a multiple of 16 and at most 256; N >= 1.
+ * NaN scores never win (an all-NaN row yields -inf and index 0).
+ */
+int gpa_sim_argmax_bf16(const void* a, const void* b,
+                        float* out_max, int64_t* out_idx,
+                        int64_t B, int64_t M, int64_t N, int64_t D,
+                        int64_t a_sb, int64_t a_sm,
+                        int64_t b_sb, int64_t b_sn,
+                        int64_t omax_sb, int64_t oidx_sb,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Attention with a per-key additive bias, head_dim 64.
+ *   o[b,h,m,:] = softmax_n( q[b,h,m,:].k[b,h,n,:] * sm_scale + bias[b,h,n] ) . v[b,h,n,:]
+ *   lse[b,h,m] = log2( sum_n 2^( (q.k*sm_scale + bias) * log2(e) ) )   (if lse != NULL)
+ * Replaces merging/fused_attention.py:130-180 (`attention_keybias`) and the
+ * Triton kernel at merging/fused_attention.py:70-127, including its log2
+ * log-sum-exp output (:123-127).  q/k/v/o are bf16; the softmax runs in fp32
+ * and P is rounded to bf16 for the P.V product, as in the reference kernel.
+ * bias_kind is GPA_BIAS_NONE (bias ignored), GPA_BIAS_F32 or GPA_BIAS_BF16;
+ * bias strides may be 0 (e.g. one bias row shared by every head).
+ */
+int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
+                          const void* bias, int bias_kind,
+                          int64_t bias_sb, int64_t bias_sh, int64_t bias_sn,
+                          void* o, float* lse,
+                          int64_t B, int64_t H, int64_t M, int64_t N, int64_t D,
+                          int64_t q_sb, int64_t q_sh, int64_t q_sm,
+                          int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                          int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                          int64_t o_sb, int64_t o_sh, int64_t o_sm,
+                          int64_t lse_sb, int64_t lse_sh,
+                          float sm_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GPA_MI355X_H */

@@ -1,0 +1,147 @@
+"""Host-side checks that need no GPU.
+
+* The C-ABI library loads and exports every function `include/gpa_mi355x.h`
+  declares; argument validation returns the documented error codes before
+  any device work.
+* The product's host logic (`merging.merge.dst_mask`, `num_dst_tokens`)
+  agrees with the oracle's step-by-step restatement of merging/merge.py.
+* The Python entry points refuse CPU tensors loudly (there is no CPU path).
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from merging import _native
+from merging.merge import dst_mask, num_dst_tokens, token_merge_bipartite2d
+from merging.fused_similarity import fused_similarity_argmax
+from merging.fused_attention import attention_keybias, LOG2E
+from oracle.merge import build_dst_mask, window_draw
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "gpa_mi355x.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gpa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _native.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(declared) == set(_native.exported_symbols())
+
+
+def test_abi_version_and_empty_error():
+    lib = _native.lib()
+    assert lib.gpa_abi_version() == _native.ABI_VERSION
+    assert lib.gpa_last_error() in (b"",) or isinstance(lib.gpa_last_error(), bytes)
+
+
+FAKE = 4096  # a 16-byte aligned non-null address; validation returns before any use
+
+
+def _sim(**kw):
+    args = dict(a=FAKE, b=FAKE, out_max=FAKE, out_idx=FAKE, B=1, M=10, N=10, D=128,
+                a_sb=1280, a_sm=128, b_sb=1280, b_sn=128, omax_sb=10, oidx_sb=10,
+                ws=None, ws_bytes=0, stream=None)
+    args.update(kw)
+    return _native.lib().gpa_sim_argmax_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=-1), _native.GPA_E_INVALID),
+    (dict(N=0), _native.GPA_E_INVALID),
+    (dict(a=None), _native.GPA_E_INVALID),
+    (dict(D=48), _native.GPA_E_UNSUPPORTED),
+    (dict(D=512, a_sm=512, b_sn=512), _native.GPA_E_UNSUPPORTED),
+    (dict(a_sm=100), _native.GPA_E_INVALID),
+    (dict(a=FAKE + 2), _native.GPA_E_INVALID),
+    (dict(M=100_000, N=100_000), _native.GPA_E_WORKSPACE),
+])
+def test_sim_argmax_argument_errors(kw, code):
+    assert _sim(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_sim_argmax_empty_problem_is_a_no_op():
+    assert _sim(M=0) == _native.GPA_OK
+    assert _sim(B=0) == _native.GPA_OK
+
+
+def test_workspace_bytes():
+    lib = _native.lib()
+    assert lib.gpa_sim_argmax_workspace_bytes(1, 10, 10, 128) == 0
+    big = lib.gpa_sim_argmax_workspace_bytes(1, 75_000, 25_000, 128)
+    assert big > 0 and big % 8 == 0
+    assert big >= 75_000 * 8                          # one (max, idx) pair per row and split
+
+
+def _attn(**kw):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, bias=None, bias_kind=0, bsb=0, bsh=0, bsn=0,
+                o=FAKE, lse=None, B=1, H=2, M=10, N=10, D=64,
+                qsb=1280, qsh=640, qsm=64, ksb=1280, ksh=640, ksn=64,
+                vsb=1280, vsh=640, vsn=64, osb=1280, osh=640, osm=64, lsb=0, lsh=0,
+                scale=0.125, stream=None)
+    args.update(kw)
+    return _native.lib().gpa_attn_keybias_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=-1), _native.GPA_E_INVALID),
+    (dict(N=0), _native.GPA_E_INVALID),
+    (dict(D=128), _native.GPA_E_UNSUPPORTED),
+    (dict(q=None), _native.GPA_E_INVALID),
+    (dict(bias_kind=7), _native.GPA_E_INVALID),
+    (dict(bias_kind=1), _native.GPA_E_INVALID),      # bias kind without a pointer
+    (dict(scale=0.0), _native.GPA_E_INVALID),
+    (dict(scale=float("nan")), _native.GPA_E_INVALID),
+    (dict(qsm=63), _native.GPA_E_INVALID),
+    (dict(k=FAKE + 8), _native.GPA_E_INVALID),
+    (dict(B=70_000), _native.GPA_E_UNSUPPORTED),
+])
+def test_attn_argument_errors(kw, code):
+    assert _attn(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_attn_empty_problem_is_a_no_op():
+    assert _attn(M=0) == _native.GPA_OK
+
+
+@pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
+    (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
+    (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
+])
+def test_product_mask_matches_oracle(frames, w, h, sx, sy, ns, no_rand):
+    g1 = torch.Generator().manual_seed(33)
+    g2 = torch.Generator().manual_seed(33)
+    mine = dst_mask(frames, w, h, sx, sy, ns, no_rand, g1, torch.device("cpu"))
+    cell = window_draw(frames, w, h, sx, sy, g2) if frames > 1 and not no_rand else None
+    ref = build_dst_mask(frames, w, h, sx, sy, ns, no_rand, cell)
+    assert torch.equal(mine, ref)
+    assert int((mine == -1).sum()) == num_dst_tokens(frames, w, h, sx, sy, ns, no_rand)
+
+
+def test_cpu_tensors_are_refused():
+    a = torch.randn(1, 8, 128)
+    with pytest.raises(AssertionError):
+        fused_similarity_argmax(a, a)
+    q = torch.randn(1, 2, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        attention_keybias(q, q, q, None, 0.125)
+    with pytest.raises(ValueError):
+        token_merge_bipartite2d(torch.randn(1, 2 * 41, 32), 6, 6, 2, 2, 5)
+    with pytest.raises(ValueError):
+        token_merge_bipartite2d(torch.randn(1, 2 * 41, 32), 6, 6, 2, 2, 0)
+
+
+def test_log2e_constant():
+    import math
+    assert LOG2E == pytest.approx(1.0 / math.log(2.0), abs=1e-15)

@@ -1,0 +1,101 @@
+"""Pins the attention oracle (oracle/attention.py) without a GPU.
+
+attention_reference is the reference's SDPA fallback with a per-key bias
+(vggt/layers/attention.py:270-276) in fp32.  It is pinned by the numpy fp64
+closed form, by SDPA itself, by the key-replication identity (a key repeated
+c times == one key with bias log c), by the LSE definition and by the exact
+LSE split identity of vggt/layers/attention.py:166-176.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.attention import (LOG2E, attention_fp64, attention_reference, kernel_inputs,
+                              lse_combine, sdpa_reference)
+
+
+def _qkv(b=1, h=2, m=40, n=33, d=64, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, h, m, d, generator=g) * scale
+    k = torch.randn(b, h, n, d, generator=g) * scale
+    v = torch.randn(b, h, n, d, generator=g)
+    bias = torch.randn(b, h, 1, n, generator=g)
+    return q, k, v, bias
+
+
+def test_reference_matches_fp64_closed_form():
+    q, k, v, bias = _qkv()
+    o, lse = attention_reference(q, k, v, bias, 0.125, q_chunk=7)
+    o64, lse64 = attention_fp64(q, k, v, bias, 0.125)
+    assert np.abs(o.numpy() - o64).max() < 2e-5
+    assert np.abs(lse.numpy() - lse64).max() < 2e-5
+
+
+def test_reference_matches_sdpa():
+    q, k, v, bias = _qkv(seed=1)
+    o, _ = attention_reference(q, k, v, bias, 0.125)
+    o_sdpa = sdpa_reference(q, k, v, bias, 0.125)
+    assert torch.allclose(o, o_sdpa, atol=2e-5)
+
+
+def test_zero_bias_is_plain_attention():
+    q, k, v, _ = _qkv(seed=2)
+    o, _ = attention_reference(q, k, v, torch.zeros(1, 2, 1, k.shape[2]), 0.125)
+    o_plain = F.scaled_dot_product_attention(q, k, v, scale=0.125)
+    assert torch.allclose(o, o_plain, atol=2e-5)
+    o_none, _ = attention_reference(q, k, v, None, 0.125)
+    assert torch.allclose(o_none, o_plain, atol=2e-5)
+
+
+def test_replication_identity():
+    """Key j repeated c_j times == key j once with bias log c_j."""
+    q, k, v, _ = _qkv(m=20, n=9, seed=3)
+    counts = torch.tensor([1, 3, 2, 5, 1, 1, 4, 2, 7])
+    rep = torch.repeat_interleave(torch.arange(9), counts)
+    o_rep = attention_fp64(q, k[:, :, rep], v[:, :, rep], None, 0.125)[0]
+    bias = counts.double().log().view(1, 1, 1, 9).expand(1, 2, 1, 9)
+    o_bias = attention_fp64(q, k, v, bias, 0.125)[0]
+    assert np.abs(o_rep - o_bias).max() < 1e-12
+    o_ref, _ = attention_reference(q, k, v, bias.float(), 0.125)
+    assert np.abs(o_ref.numpy() - o_rep).max() < 2e-5
+
+
+def test_lse_is_log2_of_denominator():
+    q, k, v, bias = _qkv(m=5, n=11, seed=4)
+    _, lse = attention_reference(q, k, v, bias, 0.125)
+    s = (q.double() @ k.double().transpose(-1, -2)) * 0.125 + bias.double()
+    expect = torch.log2(torch.exp2(s * LOG2E).sum(-1))
+    assert torch.allclose(lse.double(), expect, atol=1e-5)
+
+
+def test_lse_split_identity():
+    q, k, v, bias = _qkv(m=30, n=50, seed=5)
+    o_full, lse_full = attention_reference(q, k, v, bias, 0.125)
+    cut = 17
+    o_a, l_a = attention_reference(q, k[:, :, :cut], v[:, :, :cut], bias[..., :cut], 0.125)
+    o_b, l_b = attention_reference(q, k[:, :, cut:], v[:, :, cut:], bias[..., cut:], 0.125)
+    assert torch.allclose(lse_combine(o_a, l_a, o_b, l_b), o_full, atol=2e-5)
+    # the combined denominator is the full one
+    mx = torch.maximum(l_a, l_b)
+    assert torch.allclose(mx + torch.log2(torch.exp2(l_a - mx) + torch.exp2(l_b - mx)),
+                          lse_full, atol=1e-5)
+
+
+def test_kernel_inputs_round_fp32_to_bf16():
+    q, k, v, bias = _qkv(seed=6)
+    q2, k2, v2, b2 = kernel_inputs(q, k, v, bias)
+    assert q2.dtype == k2.dtype == v2.dtype == b2.dtype == torch.bfloat16
+    assert torch.equal(q2, q.bfloat16()) and torch.equal(b2, bias.bfloat16())
+    q3, k3, v3, _ = kernel_inputs(q.bfloat16(), k.bfloat16(), v.float(), None)
+    assert v3.dtype == torch.bfloat16
+
+
+def test_broadcast_bias_over_heads():
+    q, k, v, bias = _qkv(h=3, seed=7)
+    b1 = bias[:, :1]
+    o1, _ = attention_reference(q, k, v, b1, 0.125)
+    o2, _ = attention_reference(q, k, v, b1.expand(1, 3, 1, k.shape[2]).contiguous(), 0.125)
+    assert torch.equal(o1, o2)
