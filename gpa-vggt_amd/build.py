@@ -30,6 +30,9 @@ LIB_PATH = LIB_DIR / LIB_NAME
 ARCH = "gfx950"
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
+    # Code object v5: loadable by the HIP runtime torch bundles (ROCm 7.0)
+    # as well as by the system ROCm 7.2 runtime.
+    "-mcode-object-version=5",
     "-O3",
     "-std=c++17",
     "-fPIC",

@@ -129,6 +129,16 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _st(t: torch.Tensor, dim: int) -> int:
+    """Stride of `dim`, or 0 for a size-1 dimension (whose stride is arbitrary)."""
+    return t.stride(dim) if t.shape[dim] > 1 else 0
+
+
+def _rs(t: torch.Tensor, dim: int) -> int:
+    """Row stride of `dim`; a single row reports its own width (stride unused)."""
+    return t.stride(dim) if t.shape[dim] > 1 else t.shape[-1]
+
+
 def _rows_ok(t: torch.Tensor, align_elems: int) -> bool:
     """Unit inner stride, other strides multiples of `align_elems`, aligned base."""
     if t.stride(-1) != 1:
@@ -166,8 +176,8 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Te
     with torch.cuda.device(dev):
         rc = L.gpa_sim_argmax_bf16(
             a.data_ptr(), b.data_ptr(), out_max.data_ptr(), out_idx.data_ptr(),
-            B, M, N, D, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
-            out_max.stride(0), out_idx.stride(0),
+            B, M, N, D, _st(a, 0), _rs(a, 1), _st(b, 0), _rs(b, 1),
+            _st(out_max, 0), _st(out_idx, 0),
             ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
     _check(rc, "gpa::sim_argmax")
     return out_max, out_idx
@@ -222,7 +232,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                              f"[B,H,1,N]=[{B},{H},1,{N}]") from exc
         bias_kind = GPA_BIAS_F32 if bx.dtype == torch.float32 else GPA_BIAS_BF16
         bias_ptr = bx.data_ptr()
-        bsb, bsh, bsn = bx.stride(0), bx.stride(1), bx.stride(3)
+        bsb, bsh, bsn = _st(bx, 0), _st(bx, 1), _st(bx, 3)
     o = torch.empty(B, H, M, D, device=dev, dtype=torch.bfloat16)
     lse = (torch.empty(B, H, M, device=dev, dtype=torch.float32) if return_lse
            else torch.empty(0, device=dev, dtype=torch.float32))
@@ -233,11 +243,11 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), bias_ptr, bias_kind, bsb, bsh, bsn,
             o.data_ptr(), lse.data_ptr() if return_lse else None,
             B, H, M, N, D,
-            q.stride(0), q.stride(1), q.stride(2),
-            k.stride(0), k.stride(1), k.stride(2),
-            v.stride(0), v.stride(1), v.stride(2),
-            o.stride(0), o.stride(1), o.stride(2),
-            lse.stride(0) if return_lse else 0, lse.stride(1) if return_lse else 0,
+            _st(q, 0), _st(q, 1), _rs(q, 2),
+            _st(k, 0), _st(k, 1), _rs(k, 2),
+            _st(v, 0), _st(v, 1), _rs(v, 2),
+            _st(o, 0), _st(o, 1), _rs(o, 2),
+            _st(lse, 0) if return_lse else 0, _st(lse, 1) if return_lse else 0,
             float(sm_scale), _stream(dev))
     _check(rc, "gpa::attn_keybias")
     return o, lse
