@@ -134,14 +134,18 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
   const int nstages = n_end > n_begin ? (int)((n_end - n_begin + kTN - 1) / kTN) : 0;
   u32x4 stage[LOADS];
 
+  // Destination rows of this split through a range-checked buffer: rows past
+  // the split end read as zeros (and are masked in the epilogue).
+  const uint32_t b_row = (uint32_t)p.b_sn * 2u;
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(
+      Bm + n_begin * p.b_sn,
+      n_end > n_begin ? (uint32_t)(((n_end - n_begin - 1) * p.b_sn + D) * 2) : 0u);
   auto load_stage = [&](int st) {
-    const int64_t base = n_begin + (int64_t)st * kTN;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int id = j * 256 + tid;
       const int row = id / NCH, ch = id % NCH;
-      const int64_t n = base + row;
-      stage[j] = n < n_end ? *reinterpret_cast<const u32x4*>(Bm + n * p.b_sn + ch * 8) : u32x4{};
+      stage[j] = buf_load16(brs, (uint32_t)(st * kTN + row) * b_row + ch * 16);
     }
   };
   auto store_stage = [&](int buf) {
@@ -348,6 +352,13 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   }
 
   const SimPlan pl = make_plan(B, M, N, D);
+  // Buffer offsets are 32-bit: one split of destination rows (plus a stage
+  // of overrun) must stay below 2^31 bytes.
+  if ((pl.n_chunk + kTN) * b_sn * 2 >= ((int64_t)1 << 31)) {
+    gpa_set_error("gpa_sim_argmax_bf16: destination split exceeds 2 GiB (N=%lld, row stride %lld)",
+                  (long long)N, (long long)b_sn);
+    return GPA_E_UNSUPPORTED;
+  }
   SimArgs p{};
   p.a = (const uint16_t*)a;
   p.b = (const uint16_t*)b;

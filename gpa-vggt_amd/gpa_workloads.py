@@ -9,7 +9,9 @@ Shapes follow a VGGT-1B aggregator at 518x518: 1374 tokens per frame
                          copies of one texture, so cross-frame matches exist.
   sim_inputs             source/destination metrics for the similarity
                          kernel: tokens projected 1024 -> 128 by N(0,1)/sqrt(128),
-                         L2-normalised, bf16; every 4th token is a destination.
+                         L2-normalised, bf16; destinations are evenly spaced
+                         (token floor(i*(m+n)/n)), i.e. every 4th token at
+                         75,000 x 25,000.
   attn_inputs            biased-attention operands: Q/K/V ~ N(0,1)/sqrt(64)
                          bf16 and per-key bias log(c), c the counts of a
                          uniform multinomial assignment of M tokens to N keys
@@ -58,20 +60,19 @@ def sim_inputs(m: int = 75_000, n: int = 25_000, out_dim: int = 128, seed: int =
                device="cpu") -> Tuple[torch.Tensor, torch.Tensor]:
     """(src [1, m, out_dim], dst [1, n, out_dim]) bf16, unit rows.
 
-    Tokens come from `shifted_basis_tokens`, are projected and normalised in
-    fp32; token t is a destination when t % 4 == 0 (needs m <= 3n).
+    m + n tokens come from `shifted_basis_tokens`, are projected and
+    normalised in fp32; token floor(i * (m + n) / n) is destination i.
     """
     total = m + n
-    if m > 3 * n:
-        raise ValueError("sim_inputs: need m <= 3n (every 4th token is a destination)")
-    frames = -(-max(total, 4 * n) // TOKENS_PER_FRAME)
-    x = shifted_basis_tokens(frames, seed=seed, device=device)[0, : 4 * n]
+    frames = -(-total // TOKENS_PER_FRAME)
+    x = shifted_basis_tokens(frames, seed=seed, device=device)[0, :total]
     y = x @ projection(x.shape[-1], out_dim, seed=seed + 1, device=device)
     del x
     y = y / y.norm(dim=-1, keepdim=True)
-    is_dst = torch.arange(y.shape[0], device=device) % 4 == 0
-    dst = y[is_dst][:n]
-    src = y[~is_dst][:m]
+    is_dst = torch.zeros(total, dtype=torch.bool, device=device)
+    is_dst[torch.arange(n, device=device) * total // n] = True
+    dst = y[is_dst]
+    src = y[~is_dst]
     return src.to(torch.bfloat16).unsqueeze(0), dst.to(torch.bfloat16).unsqueeze(0)
 
 
