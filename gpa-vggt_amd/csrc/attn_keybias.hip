@@ -8,10 +8,11 @@
 // accumulation, log2 log-sum-exp output.
 //
 // Mapping onto CDNA4
-//   * A workgroup owns 256 queries of one (batch, head): 4 waves x 2 blocks
-//     of 32 queries.  Q stays in VGPRs for the whole kernel.  K, V^T and the
-//     bias stream through a 4-slot LDS ring of 32-key tiles (one barrier per
-//     tile), fed by range-checked buffer loads two tiles ahead.
+//   * A workgroup owns 256 queries of one (batch, head): 8 waves of 32
+//     queries, about 128 VGPRs each, so four waves share a SIMD and the
+//     hardware overlaps one wave's MFMAs with another's softmax.  K, V^T and
+//     the bias stream through double-buffered LDS tiles of 32 keys, fed by
+//     range-checked buffer loads one tile ahead.
 //   * Scores are computed transposed, S^T = K . Q^T, on
 //     v_mfma_f32_32x32x16_bf16: a lane owns one query and 16 of the tile's
 //     32 keys (the other 16 sit in lane^32), so the running max, the sum and
@@ -20,20 +21,15 @@
 //   * The bias enters through the accumulator input of the first QK^T MFMA
 //     (pre-divided by the exp2 scale), so adding it costs no VALU work:
 //       s = q.k + bias/sm_scale,  x = s * (sm_scale*log2 e) - m.
+//     Q stays unscaled: rounding q*sm_scale*log2(e) to bf16 would perturb
+//     sharp logits by ~2^-9 of their size.
 //   * P^T leaves the score MFMA already in the B-operand register layout of
 //     the next MFMA, O^T = V^T . P^T, provided the V^T A-operand enumerates
-//     keys in the same order; V is transposed into LDS when staged.  The
-//     output O^T also keeps one query per lane, so rescaling is a per-lane
-//     multiply.
-//   * Software pipeline: while the VALU runs the softmax of tile t, the
-//     matrix cores run QK^T of tile t+1 and P.V of tile t-1.  All three sit
-//     in one straight-line block whose instruction order is shaped with
-//     sched_group_barrier (1 MFMA : ~12 VALU).  The softmax is VALU-bound
-//     (v_exp_f32 costs about three FMAs), so this overlap is what sets speed.
-//   * The running max is updated lazily: it only moves when a tile's max
-//     exceeds it by more than kTau (log2 units), so P stays <= 2^kTau and the
-//     O rescale (a rare, wave-uniform branch after the block) runs on a
-//     handful of tiles per row instead of every tile.
+//     keys in the same order; V is transposed into LDS when staged.  O^T
+//     keeps one query per lane, so a rescale is a per-lane multiply.
+//   * The running max moves lazily: only when a tile's max exceeds it by more
+//     than kTau (log2 units), so P stays <= 2^kTau and the rescale (a rare,
+//     wave-uniform branch) runs on a handful of tiles per row.
 //   * Row sums accumulate the fp32 probabilities (before their bf16
 //     rounding), as the reference does.
 #include "gpa_common.h"
@@ -43,15 +39,15 @@
 namespace gpa {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kQB = 2;                        // 32-query blocks per wave
-constexpr int kQPerWG = kWaves * kQB * 32;    // 256 queries per workgroup
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kQPerWG = kWaves * 32;          // 256 queries per workgroup
 constexpr int kKT = 32;                       // keys per tile
 constexpr int kHD = 64;                       // head dim
 constexpr int kVTS = kKT + 4;                 // padded V^T row (elements)
-constexpr int kRing = 4;                      // LDS tile slots
 constexpr float kTau = 8.0f;                  // lazy rescale threshold (log2)
 constexpr float kPadBias = -1.0e30f;          // bias of keys past N
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
   const uint16_t* q;
@@ -70,8 +66,8 @@ struct AttnArgs {
   float bias_mul;  // log2(e) / c, i.e. 1 / sm_scale
 };
 
-// One slot of the tile ring: K rows (16-byte chunks XOR-swizzled by key),
-// V transposed (feature-major, padded rows), and the scaled bias.
+// One LDS tile: K rows (16-byte chunks XOR-swizzled by key), V transposed
+// (feature-major, padded rows), and the bias in log2 units.
 struct Tile {
   uint16_t k[kKT * kHD];
   uint16_t vt[kHD * kVTS];
@@ -83,14 +79,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
 }
 
 template <int BIAS>
-__global__ __launch_bounds__(256, 2) void attn_keybias_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) Tile ring[kRing];
+__global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) Tile ring[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, hi = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.y;
   const int64_t b = bh / p.H, h = bh % p.H;
-  const int64_t q_wave = (int64_t)blockIdx.x * kQPerWG + wave * (kQB * 32);
+  const int64_t q_row = (int64_t)blockIdx.x * kQPerWG + wave * 32 + l32;
+  const float c = p.c;
 
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
@@ -98,20 +95,16 @@ __global__ __launch_bounds__(256, 2) void attn_keybias_kernel(AttnArgs p) {
 
   // Q^T as the B-operand of S^T = K . Q^T: lane supplies query (lane%32),
   // features 16*ks + 8*hi .. +8.
-  bf16x8 qf[kQB][4];
+  bf16x8 qf[4];
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const int64_t row = q_wave + qb * 32 + l32;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qf[qb][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
-                             : bf16x8{};
-  }
+  for (int ks = 0; ks < 4; ++ks)
+    qf[ks] = q_row < p.M ? *reinterpret_cast<const bf16x8*>(Q + q_row * p.q_sm + ks * 16 + hi * 8)
+                         : bf16x8{};
 
   // Tile staging through range-checked buffer loads (keys past N read as
-  // zeros): K rows as 16-byte chunks (thread -> key tid/8, chunk tid%8); V as
-  // 2 keys x 4 features per thread, transposed on the way into LDS; the raw
-  // bias of 32 keys, scaled and padded when stored.
+  // zeros).  Waves 0-3 fetch K rows as 16-byte chunks (thread -> key t/8,
+  // chunk t%8); waves 4-7 fetch V as 2 keys x 4 features per thread,
+  // transposed on the way into LDS; threads 0-31 fetch the raw bias.
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
@@ -123,33 +116,40 @@ __global__ __launch_bounds__(256, 2) void attn_keybias_kernel(AttnArgs p) {
                 BIAS == GPA_BIAS_NONE ? 0u : p.bias_bytes);
   const uint32_t k_row = (uint32_t)p.k_sn * 2u, v_row = (uint32_t)p.v_sn * 2u;
   const uint32_t b_step = (uint32_t)p.bias_sn * (BIAS == GPA_BIAS_F32 ? 4u : 2u);
-  u32x4 kreg;
-  u32x2 vreg0, vreg1;
+  const bool k_loader = tid < 256;
+  const int u = tid & 255;
+  const int k_key = u >> 3, k_ch = u & 7;
+  const int v_kp = u >> 4, v_dq = u & 15;
+  u32x4 stg = u32x4{};  // K chunk (waves 0-3) or two V half-rows (waves 4-7)
   uint32_t braw = 0;
-  const int k_key = tid >> 3, k_ch = tid & 7;
-  const int v_kp = tid >> 4, v_dq = tid & 15;
 
   auto load_tile = [&](int t) {
     const uint32_t n0 = (uint32_t)t * kKT;
-    kreg = buf_load16(krs, (n0 + k_key) * k_row + k_ch * 16);
-    vreg0 = buf_load8(vrs, (n0 + 2 * v_kp) * v_row + v_dq * 8);
-    vreg1 = buf_load8(vrs, (n0 + 2 * v_kp + 1) * v_row + v_dq * 8);
+    if (k_loader) {
+      stg = buf_load16(krs, (n0 + k_key) * k_row + k_ch * 16);
+    } else {
+      const u32x2 v0 = buf_load8(vrs, (n0 + 2 * v_kp) * v_row + v_dq * 8);
+      const u32x2 v1 = buf_load8(vrs, (n0 + 2 * v_kp + 1) * v_row + v_dq * 8);
+      stg = u32x4{v0.x, v0.y, v1.x, v1.y};
+    }
     if (BIAS == GPA_BIAS_F32 && tid < kKT)
       braw = __builtin_amdgcn_raw_buffer_load_b32(brs, (n0 + tid) * b_step, 0, 0);
     if (BIAS == GPA_BIAS_BF16 && tid < kKT)
       braw = __builtin_amdgcn_raw_buffer_load_b16(brs, (n0 + tid) * b_step, 0, 0);
   };
-  auto store_tile = [&](int t) {
-    Tile& T = ring[t & (kRing - 1)];
-    *reinterpret_cast<u32x4*>(&T.k[k_key * kHD + ((k_ch ^ (k_key & 7)) << 3)]) = kreg;
-    // vreg0 = key 2kp: (f0|f1, f2|f3); vreg1 = key 2kp+1.  Emit, per feature,
-    // the pair (key 2kp, key 2kp+1) into row `feature` of V^T.
-    uint32_t* vt = reinterpret_cast<uint32_t*>(T.vt);
-    const int f0 = 4 * v_dq;
-    vt[((f0 + 0) * kVTS) / 2 + v_kp] = (vreg0.x & 0xffffu) | (vreg1.x << 16);
-    vt[((f0 + 1) * kVTS) / 2 + v_kp] = (vreg0.x >> 16) | (vreg1.x & 0xffff0000u);
-    vt[((f0 + 2) * kVTS) / 2 + v_kp] = (vreg0.y & 0xffffu) | (vreg1.y << 16);
-    vt[((f0 + 3) * kVTS) / 2 + v_kp] = (vreg0.y >> 16) | (vreg1.y & 0xffff0000u);
+  auto store_tile = [&](int t, Tile& T) {
+    if (k_loader) {
+      *reinterpret_cast<u32x4*>(&T.k[k_key * kHD + ((k_ch ^ (k_key & 7)) << 3)]) = stg;
+    } else {
+      // stg.xy = key 2kp: (f0|f1, f2|f3); stg.zw = key 2kp+1.  Emit, per
+      // feature, the pair (key 2kp, key 2kp+1) into row `feature` of V^T.
+      uint32_t* vt = reinterpret_cast<uint32_t*>(T.vt);
+      const int f0 = 4 * v_dq;
+      vt[((f0 + 0) * kVTS) / 2 + v_kp] = (stg.x & 0xffffu) | (stg.z << 16);
+      vt[((f0 + 1) * kVTS) / 2 + v_kp] = (stg.x >> 16) | (stg.z & 0xffff0000u);
+      vt[((f0 + 2) * kVTS) / 2 + v_kp] = (stg.y & 0xffffu) | (stg.w << 16);
+      vt[((f0 + 3) * kVTS) / 2 + v_kp] = (stg.y >> 16) | (stg.w & 0xffff0000u);
+    }
     if (tid < kKT) {
       float bv = 0.f;
       if (BIAS == GPA_BIAS_F32) bv = __uint_as_float(braw) * p.bias_mul;
@@ -158,31 +158,72 @@ __global__ __launch_bounds__(256, 2) void attn_keybias_kernel(AttnArgs p) {
     }
   };
 
-  // Scores of one tile for both query blocks: the accumulators start from
-  // the tile's bias (rows 8g + 4hi + j of the 32x32 result).
-  auto issue_qk = [&](const Tile& T, f32x16* acc) {
+  float m_run = -INFINITY;  // running max in log2 units (moved lazily)
+  float l_run = 0.f;
+  f32x16 o_acc[2] = {f32x16{}, f32x16{}};
+
+  load_tile(0);
+  store_tile(0, ring[0]);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const Tile& T = ring[t & 1];
+    if (t + 1 < ntiles) load_tile(t + 1);
+
+    // Scores: the accumulator starts from the bias of the keys this lane's
+    // registers cover (rows 8g + 4hi + j of the 32x32 result).
+    f32x16 sv;
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.bias[8 * g + 4 * hi]);
-        acc[qb][4 * g + 0] = bv[0];
-        acc[qb][4 * g + 1] = bv[1];
-        acc[qb][4 * g + 2] = bv[2];
-        acc[qb][4 * g + 3] = bv[3];
-      }
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.bias[8 * g + 4 * hi]);
+      sv[4 * g + 0] = bv[0];
+      sv[4 * g + 1] = bv[1];
+      sv[4 * g + 2] = bv[2];
+      sv[4 * g + 3] = bv[3];
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
           &T.k[l32 * kHD + (((2 * ks + hi) ^ (l32 & 7)) << 3)]);
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) acc[qb] = mfma32x32x16(kf, qf[qb][ks], acc[qb]);
+      sv = mfma32x32x16(kf, qf[ks], sv);
     }
-  };
-  // O^T += V^T . P^T for one tile.  V^T A-operand for k-step s: feature row
-  // d, keys 16s+4hi+{0..3} and 16s+8+4hi+{0..3} -- the keys whose
-  // probabilities this lane holds in its score registers 8s..8s+7.
-  auto issue_pv = [&](const Tile& T, f32x16 (*o)[2], const bf16x8 (*pb)[2]) {
+
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
+    mx = fmaxf(mx, sv[15]);
+    const float ms = max_halves(mx) * c;
+    const bool need = t == 0 || ms > m_run + kTau;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // Move m up to this tile's max and rescale what has been accumulated.
+      const float m_new = need ? ms : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      o_acc[0] *= alpha;
+      o_acc[1] *= alpha;
+    }
+
+    const float neg_m = -m_run;
+    bf16x8 pb[2];
+    float lsum = 0.f;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
+        const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
+        pb[half][e] = pp[0];
+        pb[half][e + 1] = pp[1];
+        lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
+      }
+    }
+    l_run += lsum;
+
+    // O^T += V^T . P^T.  V^T A-operand for k-step s: feature row d, keys
+    // 16s+4hi+{0..3} and 16s+8+4hi+{0..3} -- the keys whose probabilities
+    // this lane holds in its score registers 8s..8s+7.
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -191,145 +232,30 @@ __global__ __launch_bounds__(256, 2) void attn_keybias_kernel(AttnArgs p) {
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
         const bf16x4 up = *reinterpret_cast<const bf16x4*>(row + 8);
         const bf16x8 vf = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[qb][db] = mfma32x32x16(vf, pb[qb][s], o[qb][db]);
+        o_acc[db] = mfma32x32x16(vf, pb[s], o_acc[db]);
       }
-  };
 
-  float m_run[kQB], l_run[kQB];
-  f32x16 o_acc[kQB][2];
-  bf16x8 p_prev[kQB][2];
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    m_run[qb] = -INFINITY;
-    l_run[qb] = 0.f;
-    o_acc[qb][0] = f32x16{};
-    o_acc[qb][1] = f32x16{};
-    p_prev[qb][0] = bf16x8{};
-    p_prev[qb][1] = bf16x8{};
-  }
-
-  // Prologue: the slot of tile -1 holds a zero V^T (its P.V adds nothing),
-  // tiles 0 and 1 are staged, tile 2 is in flight, S(0) is issued.
-  {
-    uint32_t* vt = reinterpret_cast<uint32_t*>(ring[kRing - 1].vt);
-    for (int i = tid; i < kHD * kVTS / 2; i += 256) vt[i] = 0u;
-  }
-  load_tile(0);
-  store_tile(0);
-  load_tile(1);
-  store_tile(1);
-  __syncthreads();
-  load_tile(2);
-  f32x16 s_next[kQB];
-  issue_qk(ring[0], s_next);
-
-  const float c = p.c;
-  // One pipeline step for tile t: scores arrive in s_in (issued by the
-  // previous step), S(t+1) is issued into s_out.
-  auto step = [&](int t, f32x16* s_in, f32x16* s_out) {
-    // Matrix cores: S(t+1) and O += P(t-1).V(t-1), independent of the
-    // softmax below.  (At t = ntiles-1 the S(t+1) slot holds padding.)
-    issue_qk(ring[(t + 1) & (kRing - 1)], s_out);
-    issue_pv(ring[(t + kRing - 1) & (kRing - 1)], o_acc, p_prev);
-
-    // VALU: softmax of tile t with the lazily updated max.
-    float alpha[kQB];
-    bool need_any = false;
-#pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-      const f32x16 sv = s_in[qb];
-      float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
-#pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
-      mx = fmaxf(mx, sv[15]);
-      mx = max_halves(mx);
-      const float ms = mx * c;
-      const bool need = ms > m_run[qb] + kTau;
-      need_any |= need;
-      const float m_new = need ? ms : m_run[qb];
-      alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-      m_run[qb] = m_new;
-      const float neg_m = -m_new;
-      float lsum = 0.f;
-      bf16x8 pb[2];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
-          const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
-          pb[half][e] = pp[0];
-          pb[half][e + 1] = pp[1];
-          lsum += p0 + p1;
-        }
-      }
-      l_run[qb] = __builtin_fmaf(l_run[qb], alpha[qb], lsum);
-      p_prev[qb][0] = pb[0];
-      p_prev[qb][1] = pb[1];
-    }
-    // Shape the block -- LDS reads first, then one MFMA per dozen VALU
-    // instructions -- and end it with an empty asm that consumes the softmax
-    // results, so they are computed here rather than sunk into the next step
-    // (an asm with side effects closes the scheduling region).
-    __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
-    }
-    asm volatile("" ::"v"(p_prev[0][0]), "v"(p_prev[0][1]), "v"(p_prev[1][0]), "v"(p_prev[1][1]),
-                 "v"(l_run[0]), "v"(l_run[1]));
-
-    // Rescale O by alpha (after P(t-1).V(t-1), before P(t).V(t)): rare.
-    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) {
-        o_acc[qb][0] *= alpha[qb];
-        o_acc[qb][1] *= alpha[qb];
-      }
-    }
-
-    // Ring: slot (t+2)%4 last held tile t-2, whose reads ended before the
-    // previous barrier; tile t+3 is fetched for the next step.
-    store_tile(t + 2);
+    if (t + 1 < ntiles) store_tile(t + 1, ring[(t + 1) & 1]);
     __syncthreads();
-    load_tile(t + 3);
-  };
-
-  // Two steps per trip so the score registers alternate without copies.
-  f32x16 s_alt[kQB];
-  int t = 0;
-  for (; t + 2 <= ntiles; t += 2) {
-    step(t, s_next, s_alt);
-    step(t + 1, s_alt, s_next);
   }
-  if (t < ntiles) step(t, s_next, s_alt);
-  issue_pv(ring[(ntiles - 1) & (kRing - 1)], o_acc, p_prev);
 
-  // Epilogue: combine the two key halves of each row's sum, normalise, store.
+  // Epilogue: combine the two key halves of the row sum, normalise, store.
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+  const float l_tot = sum_halves(l_run);
+  const float inv = 1.0f / l_tot;
+  if (q_row < p.M) {
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const float l_tot = sum_halves(l_run[qb]);
-    const float inv = 1.0f / l_tot;
-    const int64_t row = q_wave + qb * 32 + l32;
-    if (row < p.M) {
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          const bf16x4 ov = {(__bf16)(o_acc[qb][db][4 * g + 0] * inv),
-                             (__bf16)(o_acc[qb][db][4 * g + 1] * inv),
-                             (__bf16)(o_acc[qb][db][4 * g + 2] * inv),
-                             (__bf16)(o_acc[qb][db][4 * g + 3] * inv)};
-          *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
-        }
-      if (p.lse && hi == 0)
-        p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_run[qb] + __log2f(l_tot);
-    }
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hi;
+        const bf16x4 ov = {(__bf16)(o_acc[db][4 * g + 0] * inv),
+                           (__bf16)(o_acc[db][4 * g + 1] * inv),
+                           (__bf16)(o_acc[db][4 * g + 2] * inv),
+                           (__bf16)(o_acc[db][4 * g + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(O + q_row * p.o_sm + d0) = ov;
+      }
+    if (p.lse && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q_row] = m_run + __log2f(l_tot);
   }
 }
 
@@ -426,11 +352,10 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   p.k_bytes = (uint32_t)(((N - 1) * k_sn + D) * 2);
   p.v_bytes = (uint32_t)(((N - 1) * v_sn + D) * 2);
   p.bias_bytes = bias_kind == GPA_BIAS_NONE ? 0u : (uint32_t)(((N - 1) * bias_sn + 1) * bias_esize);
-  const float log2e = 1.4426950408889634f;
-  p.c = sm_scale * log2e;
+  p.c = sm_scale * kLog2e;
   p.bias_mul = 1.0f / sm_scale;
 
-  const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(256);
+  const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
   hipStream_t s = (hipStream_t)stream;
   switch (bias_kind) {
     case GPA_BIAS_F32:
