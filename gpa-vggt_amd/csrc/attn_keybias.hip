@@ -30,8 +30,11 @@
 //   * The running max moves lazily: only when a tile's max exceeds it by more
 //     than kTau (log2 units), so P stays <= 2^kTau and the rescale (a rare,
 //     wave-uniform branch) runs on a handful of tiles per row.
-//   * Row sums accumulate the fp32 probabilities (before their bf16
-//     rounding), as the reference does.
+//   * Row sums: when the log-sum-exp is requested they accumulate the fp32
+//     probabilities (before their bf16 rounding), as the reference does.
+//     Otherwise they sum the bf16 P the P.V product uses, on the matrix
+//     core (4x4x4 MFMAs against ones), which takes 16 adds per tile off the
+//     VALU and normalises O by exactly the weights it was built from.
 #include "gpa_common.h"
 
 #include <math.h>
@@ -78,7 +81,7 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);
 }
 
-template <int BIAS>
+template <int BIAS, bool LSE>
 __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(16))) Tile ring[2];
 
@@ -123,19 +126,23 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   u32x4 stg = u32x4{};  // K chunk (waves 0-3) or two V half-rows (waves 4-7)
   uint32_t braw = 0;
 
+  // Per-lane byte offsets are fixed; the tile advance goes in soffset.
+  const uint32_t k_voff = k_key * k_row + k_ch * 16;
+  const uint32_t v_voff = 2 * v_kp * v_row + v_dq * 8;
+  const uint32_t b_voff = tid * b_step;
   auto load_tile = [&](int t) {
     const uint32_t n0 = (uint32_t)t * kKT;
     if (k_loader) {
-      stg = buf_load16(krs, (n0 + k_key) * k_row + k_ch * 16);
+      stg = buf_load16(krs, k_voff, n0 * k_row);
     } else {
-      const u32x2 v0 = buf_load8(vrs, (n0 + 2 * v_kp) * v_row + v_dq * 8);
-      const u32x2 v1 = buf_load8(vrs, (n0 + 2 * v_kp + 1) * v_row + v_dq * 8);
+      const u32x2 v0 = buf_load8(vrs, v_voff, n0 * v_row);
+      const u32x2 v1 = buf_load8(vrs, v_voff + v_row, n0 * v_row);
       stg = u32x4{v0.x, v0.y, v1.x, v1.y};
     }
     if (BIAS == GPA_BIAS_F32 && tid < kKT)
-      braw = __builtin_amdgcn_raw_buffer_load_b32(brs, (n0 + tid) * b_step, 0, 0);
+      braw = __builtin_amdgcn_raw_buffer_load_b32(brs, b_voff, n0 * b_step, 0);
     if (BIAS == GPA_BIAS_BF16 && tid < kKT)
-      braw = __builtin_amdgcn_raw_buffer_load_b16(brs, (n0 + tid) * b_step, 0, 0);
+      braw = __builtin_amdgcn_raw_buffer_load_b16(brs, b_voff, n0 * b_step, 0);
   };
   auto store_tile = [&](int t, Tile& T) {
     if (k_loader) {
@@ -145,29 +152,30 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       // feature, the pair (key 2kp, key 2kp+1) into row `feature` of V^T.
       uint32_t* vt = reinterpret_cast<uint32_t*>(T.vt);
       const int f0 = 4 * v_dq;
-      vt[((f0 + 0) * kVTS) / 2 + v_kp] = (stg.x & 0xffffu) | (stg.z << 16);
-      vt[((f0 + 1) * kVTS) / 2 + v_kp] = (stg.x >> 16) | (stg.z & 0xffff0000u);
-      vt[((f0 + 2) * kVTS) / 2 + v_kp] = (stg.y & 0xffffu) | (stg.w << 16);
-      vt[((f0 + 3) * kVTS) / 2 + v_kp] = (stg.y >> 16) | (stg.w & 0xffff0000u);
+      vt[((f0 + 0) * kVTS) / 2 + v_kp] = __builtin_amdgcn_perm(stg.z, stg.x, 0x05040100u);
+      vt[((f0 + 1) * kVTS) / 2 + v_kp] = __builtin_amdgcn_perm(stg.z, stg.x, 0x07060302u);
+      vt[((f0 + 2) * kVTS) / 2 + v_kp] = __builtin_amdgcn_perm(stg.w, stg.y, 0x05040100u);
+      vt[((f0 + 3) * kVTS) / 2 + v_kp] = __builtin_amdgcn_perm(stg.w, stg.y, 0x07060302u);
     }
     if (tid < kKT) {
       float bv = 0.f;
       if (BIAS == GPA_BIAS_F32) bv = __uint_as_float(braw) * p.bias_mul;
       if (BIAS == GPA_BIAS_BF16) bv = bf16_bits_to_f32(braw) * p.bias_mul;
-      T.bias[tid] = (int64_t)t * kKT + tid < p.N ? bv : kPadBias;
+      T.bias[tid] = tid < (int)min((int64_t)kKT, p.N - (int64_t)t * kKT) ? bv : kPadBias;
     }
   };
 
   float m_run = -INFINITY;  // running max in log2 units (moved lazily)
-  float l_run = 0.f;
+  float l_run = 0.f;        // LSE variant: fp32 row sum of this lane's keys
+  f32x4 l_acc = f32x4{};    // otherwise: bf16 row sum, accumulated on the MFMA
   f32x16 o_acc[2] = {f32x16{}, f32x16{}};
+  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
 
-  load_tile(0);
-  store_tile(0, ring[0]);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const Tile& T = ring[t & 1];
+  // One tile: scores, softmax, P.V; then stage tile t+1 into `Tn` (last read
+  // before the previous barrier) and synchronise.  Both ring slots are
+  // compile-time objects in the unrolled loop below, so every LDS address
+  // is a loop-invariant register plus an immediate offset.
+  auto step = [&](const Tile& T, Tile& Tn, const int t) {
     if (t + 1 < ntiles) load_tile(t + 1);
 
     // Scores: the accumulator starts from the bias of the keys this lane's
@@ -199,7 +207,10 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       const float m_new = need ? ms : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
-      l_run *= alpha;
+      if (LSE)
+        l_run *= alpha;
+      else
+        l_acc *= alpha;
       o_acc[0] *= alpha;
       o_acc[1] *= alpha;
     }
@@ -216,10 +227,18 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
         const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
         pb[half][e] = pp[0];
         pb[half][e + 1] = pp[1];
-        lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
+        if (LSE) lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
       }
     }
-    l_run += lsum;
+    if (LSE) {
+      l_run += lsum;
+    } else {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        l_acc = mfma4x4x4(ones4, bf16x4{pb[half][0], pb[half][1], pb[half][2], pb[half][3]}, l_acc);
+        l_acc = mfma4x4x4(ones4, bf16x4{pb[half][4], pb[half][5], pb[half][6], pb[half][7]}, l_acc);
+      }
+    }
 
     // O^T += V^T . P^T.  V^T A-operand for k-step s: feature row d, keys
     // 16s+4hi+{0..3} and 16s+8+4hi+{0..3} -- the keys whose probabilities
@@ -235,9 +254,20 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
         o_acc[db] = mfma32x32x16(vf, pb[s], o_acc[db]);
       }
 
-    if (t + 1 < ntiles) store_tile(t + 1, ring[(t + 1) & 1]);
+    if (t + 1 < ntiles) store_tile(t + 1, Tn);
     __syncthreads();
+  };
+
+  load_tile(0);
+  store_tile(0, ring[0]);
+  __syncthreads();
+  int t = 0;
+  for (; t + 2 <= ntiles; t += 2) {
+    step(ring[0], ring[1], t);
+    step(ring[1], ring[0], t + 1);
   }
+  if (t < ntiles) step(ring[0], ring[1], t);
+  if (!LSE) l_run = l_acc[0];
 
   // Epilogue: combine the two key halves of the row sum, normalise, store.
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
@@ -357,17 +387,24 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
   hipStream_t s = (hipStream_t)stream;
+  const bool want_lse = lse != nullptr;
+#define GPA_ATTN_LAUNCH(KIND)                                                          \
+  if (want_lse)                                                                        \
+    hipLaunchKernelGGL((attn_keybias_kernel<KIND, true>), grid, block, 0, s, p);       \
+  else                                                                                 \
+    hipLaunchKernelGGL((attn_keybias_kernel<KIND, false>), grid, block, 0, s, p);
   switch (bias_kind) {
     case GPA_BIAS_F32:
-      hipLaunchKernelGGL(attn_keybias_kernel<GPA_BIAS_F32>, grid, block, 0, s, p);
+      GPA_ATTN_LAUNCH(GPA_BIAS_F32);
       break;
     case GPA_BIAS_BF16:
-      hipLaunchKernelGGL(attn_keybias_kernel<GPA_BIAS_BF16>, grid, block, 0, s, p);
+      GPA_ATTN_LAUNCH(GPA_BIAS_BF16);
       break;
     default:
-      hipLaunchKernelGGL(attn_keybias_kernel<GPA_BIAS_NONE>, grid, block, 0, s, p);
+      GPA_ATTN_LAUNCH(GPA_BIAS_NONE);
       break;
   }
+#undef GPA_ATTN_LAUNCH
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("gpa_attn_keybias_bf16: launch failed: %s", hipGetErrorString(e));

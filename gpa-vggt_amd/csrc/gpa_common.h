@@ -38,6 +38,13 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// 16 independent 4x4x4 blocks, bf16 operands, fp32 accumulate.  With an
+// all-ones A operand every lane receives the sum of its own four B values
+// (in all four result registers).
+__device__ __forceinline__ f32x4 mfma4x4x4(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
 // Raw buffer resource over `bytes` bytes at `base`.  Loads through it are
 // range-checked by the hardware: an access at or past `bytes` returns zeros,
 // so tile prefetches need neither branches nor index clamps.
@@ -46,12 +53,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            0x00020000);
 }
 
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+// Loads at byte offset voff + soff: voff per lane, soff wave-uniform (SGPR),
+// so a per-tile advance costs no vector ALU work.
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
 
-__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                           uint32_t soff = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
 }
 
 // v_permlane32_swap on one value: lanes l and l^32 exchange.  The builtin

@@ -60,11 +60,14 @@ def test_matches_fp32_reference(dev, B, H, M, N, bias):
 
 
 def test_output_without_lse_matches(dev):
+    """Without the LSE the row sum is taken over the bf16 P (on the matrix
+    core), with it over the fp32 P: the outputs agree to bf16 rounding."""
     q, k, v, b = _inputs(1, 2, 200, 300, seed=1)
     args = (q.to(dev), k.to(dev), v.to(dev), b.to(dev), 0.125)
     o1 = attention_keybias(*args)
     o2, _ = attention_keybias(*args, return_lse=True)
-    assert torch.equal(o1, o2)
+    err = (o1.float() - o2.float()).abs()
+    assert err.max().item() < 2e-2 and err.mean().item() < 1e-3
 
 
 def test_sharp_logits_and_large_bias(dev):
