@@ -18,11 +18,14 @@
 //     32 keys (the other 16 sit in lane^32), so the running max, the sum and
 //     the rescale factor are per-lane scalars; the two halves meet through
 //     v_permlane32_swap.
-//   * The bias enters through the accumulator input of the first QK^T MFMA
-//     (pre-divided by the exp2 scale), so adding it costs no VALU work:
-//       s = q.k + bias/sm_scale,  x = s * (sm_scale*log2 e) - m.
-//     Q stays unscaled: rounding q*sm_scale*log2(e) to bf16 would perturb
-//     sharp logits by ~2^-9 of their size.
+//   * The bias rides in a fifth k-step of the score MFMA: each key carries
+//     bias/sm_scale split into a bf16 hi/lo pair, multiplied by a constant
+//     (1, 1) column of Q, so
+//       s = q.k + bias/sm_scale,  x = s * (sm_scale*log2 e) - m
+//     costs no VALU work and one 4-byte LDS read per lane per tile (instead
+//     of four 16-byte broadcast reads of an fp32 bias row).  Q stays
+//     unscaled: rounding q*sm_scale*log2(e) to bf16 would perturb sharp
+//     logits by ~2^-9 of their size.
 //   * P^T leaves the score MFMA already in the B-operand register layout of
 //     the next MFMA, O^T = V^T . P^T, provided the V^T A-operand enumerates
 //     keys in the same order; V is transposed into LDS when staged.  O^T
@@ -32,9 +35,10 @@
 //     wave-uniform branch) runs on a handful of tiles per row.
 //   * Row sums: when the log-sum-exp is requested they accumulate the fp32
 //     probabilities (before their bf16 rounding), as the reference does.
-//     Otherwise they sum the bf16 P the P.V product uses, on the matrix
-//     core (4x4x4 MFMAs against ones), which takes 16 adds per tile off the
-//     VALU and normalises O by exactly the weights it was built from.
+//     Otherwise they sum the bf16 P the P.V product uses with
+//     v_dot2_f32_bf16 (exact fp32 sums of bf16 pairs, 8 instead of 16 VALU
+//     instructions per tile), normalising O by exactly the weights it was
+//     built from.
 #include "gpa_common.h"
 
 #include <math.h>
@@ -70,12 +74,21 @@ struct AttnArgs {
 };
 
 // One LDS tile: K rows (16-byte chunks XOR-swizzled by key), V transposed
-// (feature-major, padded rows), and the bias in log2 units.
-struct Tile {
+// (feature-major, padded rows), and per key the bias/sm_scale as a packed
+// bf16 (hi, lo) pair; slot kKT stays zero for the lanes whose fifth-k-step
+// operand is empty.
+struct alignas(16) Tile {
   uint16_t k[kKT * kHD];
   uint16_t vt[kHD * kVTS];
-  float bias[kKT];
+  uint32_t bias[kKT + 1];
 };
+
+// XOR swizzle of K's 16-byte chunks: lanes reading one logical chunk of 16
+// consecutive keys hit 16 distinct 16-byte bank groups (64 banks), and any
+// 8 consecutive keys hit 8 distinct ones (32 banks).
+__device__ __forceinline__ int k_chunk(int key, int ch) {
+  return ch ^ (key & 7) ^ ((key >> 3) & 1);
+}
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);
@@ -103,6 +116,14 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   for (int ks = 0; ks < 4; ++ks)
     qf[ks] = q_row < p.M ? *reinterpret_cast<const bf16x8*>(Q + q_row * p.q_sm + ks * 16 + hi * 8)
                          : bf16x8{};
+  // Fifth k-step: Q supplies (1, 1) against each key's (bias_hi, bias_lo),
+  // on the low half only (k = 64, 65).
+  bf16x8 q_bias = bf16x8{};
+  if (hi == 0) {
+    q_bias[0] = (__bf16)1.0f;
+    q_bias[1] = (__bf16)1.0f;
+  }
+  const int bias_slot = hi == 0 ? l32 : kKT;  // slot kKT holds zero
 
   // Tile staging through range-checked buffer loads (keys past N read as
   // zeros).  Waves 0-3 fetch K rows as 16-byte chunks (thread -> key t/8,
@@ -146,7 +167,7 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   };
   auto store_tile = [&](int t, Tile& T) {
     if (k_loader) {
-      *reinterpret_cast<u32x4*>(&T.k[k_key * kHD + ((k_ch ^ (k_key & 7)) << 3)]) = stg;
+      *reinterpret_cast<u32x4*>(&T.k[k_key * kHD + (k_chunk(k_key, k_ch) << 3)]) = stg;
     } else {
       // stg.xy = key 2kp: (f0|f1, f2|f3); stg.zw = key 2kp+1.  Emit, per
       // feature, the pair (key 2kp, key 2kp+1) into row `feature` of V^T.
@@ -161,15 +182,18 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       float bv = 0.f;
       if (BIAS == GPA_BIAS_F32) bv = __uint_as_float(braw) * p.bias_mul;
       if (BIAS == GPA_BIAS_BF16) bv = bf16_bits_to_f32(braw) * p.bias_mul;
-      T.bias[tid] = tid < (int)min((int64_t)kKT, p.N - (int64_t)t * kKT) ? bv : kPadBias;
+      bv = tid < (int)min((int64_t)kKT, p.N - (int64_t)t * kKT) ? bv : kPadBias;
+      const __bf16 bhi = (__bf16)bv;
+      const __bf16 blo = (__bf16)(bv - (float)bhi);
+      T.bias[tid] = (uint32_t)__builtin_bit_cast(uint16_t, bhi) |
+                    ((uint32_t)__builtin_bit_cast(uint16_t, blo) << 16);
     }
   };
 
   float m_run = -INFINITY;  // running max in log2 units (moved lazily)
   float l_run = 0.f;        // LSE variant: fp32 row sum of this lane's keys
-  f32x4 l_acc = f32x4{};    // otherwise: bf16 row sum, accumulated on the MFMA
   f32x16 o_acc[2] = {f32x16{}, f32x16{}};
-  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 
   // One tile: scores, softmax, P.V; then stage tile t+1 into `Tn` (last read
   // before the previous barrier) and synchronise.  Both ring slots are
@@ -178,22 +202,18 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   auto step = [&](const Tile& T, Tile& Tn, const int t) {
     if (t + 1 < ntiles) load_tile(t + 1);
 
-    // Scores: the accumulator starts from the bias of the keys this lane's
-    // registers cover (rows 8g + 4hi + j of the 32x32 result).
-    f32x16 sv;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.bias[8 * g + 4 * hi]);
-      sv[4 * g + 0] = bv[0];
-      sv[4 * g + 1] = bv[1];
-      sv[4 * g + 2] = bv[2];
-      sv[4 * g + 3] = bv[3];
-    }
+    // Scores s = q.k + bias/sm_scale (rows 8g + 4hi + j of the 32x32 result).
+    f32x16 sv = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-          &T.k[l32 * kHD + (((2 * ks + hi) ^ (l32 & 7)) << 3)]);
+      const bf16x8 kf =
+          *reinterpret_cast<const bf16x8*>(&T.k[l32 * kHD + (k_chunk(l32, 2 * ks + hi) << 3)]);
       sv = mfma32x32x16(kf, qf[ks], sv);
+    }
+    {
+      const uint32_t pair = T.bias[bias_slot];
+      const u32x4 kb = {pair, 0u, 0u, 0u};
+      sv = mfma32x32x16(__builtin_bit_cast(bf16x8, kb), q_bias, sv);
     }
 
     float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
@@ -207,10 +227,7 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       const float m_new = need ? ms : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
-      if (LSE)
-        l_run *= alpha;
-      else
-        l_acc *= alpha;
+      l_run *= alpha;
       o_acc[0] *= alpha;
       o_acc[1] *= alpha;
     }
@@ -227,18 +244,13 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
         const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
         pb[half][e] = pp[0];
         pb[half][e + 1] = pp[1];
-        if (LSE) lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
+        if (LSE)
+          lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
+        else
+          lsum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones2, lsum, false);
       }
     }
-    if (LSE) {
-      l_run += lsum;
-    } else {
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        l_acc = mfma4x4x4(ones4, bf16x4{pb[half][0], pb[half][1], pb[half][2], pb[half][3]}, l_acc);
-        l_acc = mfma4x4x4(ones4, bf16x4{pb[half][4], pb[half][5], pb[half][6], pb[half][7]}, l_acc);
-      }
-    }
+    l_run += lsum;
 
     // O^T += V^T . P^T.  V^T A-operand for k-step s: feature row d, keys
     // 16s+4hi+{0..3} and 16s+8+4hi+{0..3} -- the keys whose probabilities
@@ -258,6 +270,10 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
     __syncthreads();
   };
 
+  if (tid == 0) {
+    ring[0].bias[kKT] = 0u;
+    ring[1].bias[kKT] = 0u;
+  }
   load_tile(0);
   store_tile(0, ring[0]);
   __syncthreads();
@@ -267,7 +283,6 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
     step(ring[1], ring[0], t + 1);
   }
   if (t < ntiles) step(ring[0], ring[1], t);
-  if (!LSE) l_run = l_acc[0];
 
   // Epilogue: combine the two key halves of the row sum, normalise, store.
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
