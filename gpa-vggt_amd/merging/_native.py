@@ -23,7 +23,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -61,6 +61,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _i64, _i64,                    # omax_sb, oidx_sb
         _vp, ctypes.c_size_t, _vp,     # workspace, workspace_bytes, stream
     ]
+    lib.gpa_attn_keybias_workspace_bytes.restype = ctypes.c_size_t
+    lib.gpa_attn_keybias_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int, _i64, _i64]
     lib.gpa_attn_keybias_bf16.restype = ctypes.c_int
     lib.gpa_attn_keybias_bf16.argtypes = [
         _vp, _vp, _vp,                 # q, k, v
@@ -73,6 +75,7 @@ def _bind(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64,              # v strides
         _i64, _i64, _i64,              # o strides
         _i64, _i64,                    # lse strides
+        _vp, ctypes.c_size_t,          # workspace, workspace_bytes
         ctypes.c_float, _vp,           # sm_scale, stream
     ]
 
@@ -100,7 +103,7 @@ def lib() -> ctypes.CDLL:
 
 def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
-            "gpa_sim_argmax_bf16", "gpa_attn_keybias_bf16")
+            "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -219,7 +222,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         q = q.contiguous()
     if not _rows_ok(k, 8):
         k = k.contiguous()
-    if not _rows_ok(v, 4):
+    if not _rows_ok(v, 8):
         v = v.contiguous()
     bias_kind, bias_ptr, bsb, bsh, bsn = GPA_BIAS_NONE, None, 0, 0, 0
     if bias is not None:
@@ -238,8 +241,11 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
            else torch.empty(0, device=dev, dtype=torch.float32))
     if B == 0 or H == 0 or M == 0:
         return o, lse
+    L = lib()
+    ws_bytes = L.gpa_attn_keybias_workspace_bytes(B, H, N, bias_kind, bsb, bsh)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
-        rc = lib().gpa_attn_keybias_bf16(
+        rc = L.gpa_attn_keybias_bf16(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), bias_ptr, bias_kind, bsb, bsh, bsn,
             o.data_ptr(), lse.data_ptr() if return_lse else None,
             B, H, M, N, D,
@@ -248,7 +254,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             _st(v, 0), _st(v, 1), _rs(v, 2),
             _st(o, 0), _st(o, 1), _rs(o, 2),
             _st(lse, 0) if return_lse else 0, _st(lse, 1) if return_lse else 0,
-            float(sm_scale), _stream(dev))
+            ws.data_ptr(), ws_bytes, float(sm_scale), _stream(dev))
     _check(rc, "gpa::attn_keybias")
     return o, lse
 

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 1
+#define GPA_ABI_VERSION 2
 
 enum {
   GPA_OK = 0,
@@ -64,7 +64,7 @@ size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D
  * Replaces merging/fused_similarity.py:81-112 (`fused_similarity_argmax`);
  * the index tie rule follows the kernel's strict `>` at
  * merging/fused_similarity.py:73 together with tl.argmax's first index.
- * D must be a multiple of 16 and at most 256; N >= 1.
+ * D must be a multiple of 32 and at most 256; N >= 1.
  * NaN scores never win (an all-NaN row yields -inf and index 0).
  */
 int gpa_sim_argmax_bf16(const void* a, const void* b,
@@ -76,6 +76,13 @@ int gpa_sim_argmax_bf16(const void* a, const void* b,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Bytes of device workspace gpa_attn_keybias_bf16 needs: the padded buffer
+ * of per-key bias pairs (one row per batch/head with its own bias; the
+ * reference wrapper allocates the same kind of buffer,
+ * merging/fused_attention.py:159-160). */
+size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t N, int bias_kind,
+                                        int64_t bias_sb, int64_t bias_sh);
+
 /*
  * Attention with a per-key additive bias, head_dim 64.
  *   o[b,h,m,:] = softmax_n( q[b,h,m,:].k[b,h,n,:] * sm_scale + bias[b,h,n] ) . v[b,h,n,:]
@@ -86,6 +93,8 @@ int gpa_sim_argmax_bf16(const void* a, const void* b,
  * and P is rounded to bf16 for the P.V product, as in the reference kernel.
  * bias_kind is GPA_BIAS_NONE (bias ignored), GPA_BIAS_F32 or GPA_BIAS_BF16;
  * bias strides may be 0 (e.g. one bias row shared by every head).
+ * workspace: 16-byte aligned device memory of at least
+ * gpa_attn_keybias_workspace_bytes(...) bytes, overwritten by the call.
  */
 int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
                           const void* bias, int bias_kind,
@@ -97,6 +106,7 @@ int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
                           int64_t v_sb, int64_t v_sh, int64_t v_sn,
                           int64_t o_sb, int64_t o_sh, int64_t o_sm,
                           int64_t lse_sb, int64_t lse_sh,
+                          void* workspace, size_t workspace_bytes,
                           float sm_scale, void* stream);
 
 #ifdef __cplusplus

@@ -88,7 +88,7 @@ def _attn(**kw):
                 o=FAKE, lse=None, B=1, H=2, M=10, N=10, D=64,
                 qsb=1280, qsh=640, qsm=64, ksb=1280, ksh=640, ksn=64,
                 vsb=1280, vsh=640, vsn=64, osb=1280, osh=640, osm=64, lsb=0, lsh=0,
-                scale=0.125, stream=None)
+                ws=FAKE, ws_bytes=1 << 20, scale=0.125, stream=None)
     args.update(kw)
     return _native.lib().gpa_attn_keybias_bf16(*args.values())
 
@@ -105,6 +105,9 @@ def _attn(**kw):
     (dict(qsm=63), _native.GPA_E_INVALID),
     (dict(k=FAKE + 8), _native.GPA_E_INVALID),
     (dict(B=70_000), _native.GPA_E_UNSUPPORTED),
+    (dict(ws=None), _native.GPA_E_WORKSPACE),
+    (dict(ws_bytes=16), _native.GPA_E_WORKSPACE),
+    (dict(v=FAKE + 8), _native.GPA_E_INVALID),
 ])
 def test_attn_argument_errors(kw, code):
     assert _attn(**kw) == code
@@ -113,6 +116,15 @@ def test_attn_argument_errors(kw, code):
 
 def test_attn_empty_problem_is_a_no_op():
     assert _attn(M=0) == _native.GPA_OK
+
+
+def test_attn_workspace_bytes():
+    lib = _native.lib()
+    # one row of bias pairs per (batch, head), keys padded to whole 32-key tiles
+    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 68_700, 2, 16 * 68_700, 68_700) == 16 * 68_704 * 4
+    # a bias shared by every head, or no bias, needs a single row
+    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 100, 1, 100, 0) == 128 * 4
+    assert lib.gpa_attn_keybias_workspace_bytes(2, 16, 100, 0, 0, 0) == 128 * 4
 
 
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
