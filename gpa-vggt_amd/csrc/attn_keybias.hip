@@ -6,15 +6,15 @@
 // Semantics follow merging/fused_attention.py:70-127: scores in the exp2
 // domain, fp32 online softmax, P rounded to bf16 for the P.V product, fp32
 // accumulation, log2 log-sum-exp output.  Like the reference wrapper
-// (fused_attention.py:159-160), the bias is first written to a padded
-// per-key buffer -- here bias/sm_scale as bf16 (hi, lo) pairs, with the keys
-// past N padded to -1e30 -- by a small pre-pass.
+// (fused_attention.py:159-160), a small pre-pass first writes the bias to a
+// padded per-key buffer; here each 32-key tile gets a 144-byte record: the
+// 32 values bias/sm_scale (-inf past N) and the tile's score bound below.
 //
 // Mapping onto CDNA4
 //   * A workgroup owns 256 queries of one (batch, head): 8 waves of 32
 //     queries, <= 128 VGPRs each, so four waves share a SIMD and the
 //     hardware overlaps one wave's MFMAs with another's softmax.
-//   * K, V and the bias pairs stream through a 4-slot LDS ring of 32-key
+//   * K, V and the tile records stream through a 4-slot LDS ring of 32-key
 //     tiles filled by buffer_load ... lds (DMA into LDS, no staging
 //     registers) three tiles ahead of the one being computed.  Keeping
 //     three tiles (24 KB) in flight per workgroup is what hides the L2/HBM
@@ -24,12 +24,11 @@
 //     v_mfma_f32_32x32x16_bf16: a lane owns one query and 16 of the tile's
 //     32 keys (the other 16 sit in lane^32), so the running max, the sum and
 //     the rescale factor are per-lane scalars; the two halves meet through
-//     v_permlane32_swap.
-//   * The bias rides in a fifth k-step of the score MFMA: each key's
-//     (bias_hi, bias_lo) pair times a constant (1, 1) column of Q gives
-//       s = q.k + bias/sm_scale,  x = s * (sm_scale*log2 e) - m
-//     at no VALU cost.  Q stays unscaled: rounding q*sm_scale*log2(e) to
-//     bf16 would perturb sharp logits by ~2^-9 of their size.
+//     v_permlane32_swap.  The accumulator starts from the tile's fp32
+//     bias/sm_scale values (four broadcast LDS reads), so the MFMA chain
+//     yields s = q.k + bias/sm_scale and x = s * (sm_scale*log2 e) - m is
+//     one FMA.  Q stays unscaled: rounding q*sm_scale*log2(e) to bf16 would
+//     perturb sharp logits by ~2^-9 of their size.
 //   * P^T leaves the score MFMA already in the B-operand register layout of
 //     the next MFMA, O^T = V^T . P^T, when the V^T A-operand enumerates keys
 //     in the same order.  V stays row-major in LDS and the V^T operand is
@@ -37,9 +36,15 @@
 //     4v+a loads four features of key base+v and lane i receives feature
 //     c0+i of keys base..base+3.  O^T keeps one query per lane, so a
 //     rescale is a per-lane multiply.
-//   * The running max moves lazily: only when a tile's max exceeds it by more
-//     than kTau (log2 units), so P stays <= 2^kTau and the rescale (a rare,
-//     wave-uniform branch) runs on a handful of tiles per row.
+//   * The softmax offset m only has to keep 2^(x-m) in range, since P is
+//     stored in bf16, which has fp32's exponent range: m moves lazily, only
+//     when a tile could produce x > m + kTau.  Whether it could is decided
+//     from a Cauchy-Schwarz bound, x <= c*(|q| max|k| + max bias/sm_scale)
+//     over the tile's keys (the record carries both maxima), one FMA per
+//     lane; only when the bound exceeds m + kTau does the wave take the exact
+//     row max and, where it is above m + kTau, rescale (a rare, wave-uniform
+//     branch).  The result is the same softmax; only the (arbitrary) offset
+//     differs from the reference's running max.
 //   * Row sums: with the log-sum-exp requested they accumulate the fp32
 //     probabilities (before their bf16 rounding), as the reference does;
 //     otherwise they sum the bf16 P the P.V product uses with
@@ -52,6 +57,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace gpa {
 namespace {
 
@@ -62,40 +69,49 @@ constexpr int kKT = 32;                       // keys per tile
 constexpr int kHD = 64;                       // head dim
 constexpr int kRing = 4;                      // LDS tile slots
 constexpr int kAhead = kRing - 1;             // tiles in flight beyond the current one
-constexpr float kTau = 8.0f;                  // lazy rescale threshold (log2)
-constexpr float kPadBias = -1.0e30f;          // bias of keys past N
+constexpr float kTau = 16.0f;                 // lazy rescale threshold (log2): P <= 2^kTau
+constexpr float kMInit = -1.0e30f;            // finite initial offset (all -inf rows give 0)
+constexpr float kGap = 64.0f;                 // largest offset above the row max a fixed m may have
+constexpr int kRec = 36;                      // words per tile record
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
-  const uint32_t* pairs;  // [rows][npad] bias pairs
+  const float* recs;      // [B*H][ntiles][kRec] tile records
+  const float* bounds;    // [B*H][2] maxima of the records' words 32 and 33
+  uint8_t* flags;         // [B*H][gx][8] per wave: 1 = rows left to the lazy pass
   uint16_t* o;
   float* lse;
   int H;
   int64_t M, N;
   int64_t q_sb, q_sh, q_sm, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sm;
-  int64_t pairs_sb, pairs_sh, lse_sb, lse_sh;
-  uint32_t k_bytes, v_bytes, pair_bytes;  // extent of one (batch, head) slice
+  int64_t lse_sb, lse_sh;
+  uint32_t k_bytes, v_bytes, rec_bytes;  // extent of one (batch, head) slice
   float c;                                // sm_scale * log2(e)
 };
 
-struct PairArgs {
+struct RecArgs {
+  const uint16_t* k;
   const void* bias;
-  uint32_t* pairs;
+  float* recs;
   int kind;
-  int rows_h;  // heads with their own pair row (1 or H)
-  int64_t sb, sh, sn;
-  int64_t N, npad, total;
+  int H;
+  int64_t k_sb, k_sh, k_sn;
+  int64_t sb, sh, sn;  // bias strides (0 = broadcast)
+  int64_t N, ntiles, total_keys;
   float mul;  // 1 / sm_scale
+  float c;    // sm_scale * log2(e)
 };
 
 // One slot of the tile ring.
 struct alignas(16) Tile {
   uint16_t k[kKT * kHD];  // key rows, 16-byte chunks swizzled by k_chunk
   uint16_t v[kKT * kHD];  // value rows, 16-byte chunks swizzled by v_chunk
-  uint32_t bias[kKT];     // (bias_hi | bias_lo << 16) per key
+  // [0, 32): bias/sm_scale per key; [32]: c*max|k|; [33]: c*max bias/sm_scale;
+  // [34, 36): zero.
+  float rec[kRec];
 };
 
 // K chunk swizzle: 16 consecutive keys reading one logical chunk hit 16
@@ -113,13 +129,6 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);
 }
 
-__device__ __forceinline__ uint32_t bias_pair(float x) {
-  const __bf16 bhi = (__bf16)x;
-  const __bf16 blo = (__bf16)(x - (float)bhi);
-  return (uint32_t)__builtin_bit_cast(uint16_t, bhi) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, blo) << 16);
-}
-
 // DMA of 16 bytes per lane into LDS at lds + 16*lane.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff,
                                       uint32_t soff) {
@@ -135,13 +144,15 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__global__ __launch_bounds__(256) void bias_pairs_kernel(PairArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.total) return;
-  const int64_t n = i % a.npad, row = i / a.npad;
-  const int64_t hb = row % a.rows_h, bb = row / a.rows_h;
-  float x = kPadBias;
-  if (n < a.N) {
+// Tile records: one thread per key; the 32 lanes of a tile reduce the two
+// maxima with cross-lane shuffles.  Keys past N get bias -inf and |k| = 0.
+__global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B*H*ntiles*32
+  const bool live = i < a.total_keys;
+  const int64_t n = i % (a.ntiles * kKT), row = i / (a.ntiles * kKT);
+  const int64_t hb = row % a.H, bb = row / a.H;
+  float x = -INFINITY, kn = 0.f;
+  if (live && n < a.N) {
     const int64_t off = bb * a.sb + hb * a.sh + n * a.sn;
     if (a.kind == GPA_BIAS_F32)
       x = static_cast<const float*>(a.bias)[off] * a.mul;
@@ -149,8 +160,55 @@ __global__ __launch_bounds__(256) void bias_pairs_kernel(PairArgs a) {
       x = bf16_bits_to_f32(static_cast<const uint16_t*>(a.bias)[off]) * a.mul;
     else
       x = 0.f;
+    const bf16x8* kr = reinterpret_cast<const bf16x8*>(a.k + bb * a.k_sb + hb * a.k_sh + n * a.k_sn);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kHD / 8; ++j) {
+      const bf16x8 v = kr[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)v[e], (float)v[e], ss);
+    }
+    kn = __builtin_sqrtf(ss);
   }
-  a.pairs[i] = bias_pair(x);
+  float kmax = kn, xmax = x;
+#pragma unroll
+  for (int w = 1; w < kKT; w <<= 1) {
+    kmax = fmaxf(kmax, __shfl_xor(kmax, w, kKT));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, w, kKT));
+  }
+  if (!live) return;
+  float* rec = a.recs + (row * a.ntiles + n / kKT) * kRec;
+  const int j = (int)(n % kKT);
+  rec[j] = x;
+  if (j < kRec - kKT) rec[kKT + j] = j == 0 ? a.c * kmax : j == 1 ? a.c * xmax : 0.f;
+}
+
+// Per (batch, head): the maxima over its tiles of c*max|k| and
+// c*max bias/sm_scale, so c*(|q| K + B) bounds every score of a query.
+__global__ __launch_bounds__(256) void row_bounds_kernel(const float* recs, float* bounds,
+                                                         int64_t ntiles) {
+  __shared__ float part[2][4];
+  const float* r = recs + (int64_t)blockIdx.x * ntiles * kRec;
+  float kb = 0.f, bb = -INFINITY;
+  for (int64_t t = threadIdx.x; t < ntiles; t += 256) {
+    kb = fmaxf(kb, r[t * kRec + kKT]);
+    bb = fmaxf(bb, r[t * kRec + kKT + 1]);
+  }
+#pragma unroll
+  for (int w = 1; w < 64; w <<= 1) {
+    kb = fmaxf(kb, __shfl_xor(kb, w));
+    bb = fmaxf(bb, __shfl_xor(bb, w));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    part[0][threadIdx.x >> 6] = kb;
+    part[1][threadIdx.x >> 6] = bb;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    bounds[2 * blockIdx.x] = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
+    bounds[2 * blockIdx.x + 1] =
+        fmaxf(fmaxf(part[1][0], part[1][1]), fmaxf(part[1][2], part[1][3]));
+  }
 }
 
 // Workgroup barrier that does not drain the vector-memory counter: the
@@ -162,7 +220,12 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <bool LSE>
+// LAZY = false: the main pass.  Every wave uses the fixed offset when tile 0
+// certifies it; a wave that cannot certify it stores nothing and sets its
+// flag.  LAZY = true: the repair pass.  Workgroups without a flagged wave
+// exit at once; the others recompute their rows with the lazily moved
+// offset, and the flagged waves store theirs.
+template <bool LSE, bool LAZY>
 __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   // Four separate LDS objects (not one array) so the compiler's LDS-DMA
   // tracking can tell which slot a DMA writes and which a read reads.
@@ -174,13 +237,20 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.y;
   const int64_t b = bh / p.H, h = bh % p.H;
+  uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
+  bool store = true;
+  if constexpr (LAZY) {
+    const uint64_t f = *reinterpret_cast<const uint64_t*>(flag_row);
+    if (f == 0) return;  // workgroup-uniform: before any barrier or DMA
+    store = ((f >> (8 * wave)) & 0xff) != 0;
+  }
   const int64_t q_row = (int64_t)blockIdx.x * kQPerWG + wave * 32 + l32;
   const float c = p.c;
 
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
-  const uint32_t* P = p.pairs + b * p.pairs_sb + h * p.pairs_sh;
+  const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
 
   // Q^T as the B-operand of S^T = K . Q^T: lane supplies query (lane%32),
   // features 16*ks + 8*hi .. +8.
@@ -189,20 +259,20 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   for (int ks = 0; ks < 4; ++ks)
     qf[ks] = q_row < p.M ? *reinterpret_cast<const bf16x8*>(Q + q_row * p.q_sm + ks * 16 + hi * 8)
                          : bf16x8{};
-  // Fifth k-step: Q supplies (1, 1) against each key's (bias_hi, bias_lo),
-  // on the low half only (k = 64, 65).
-  bf16x8 q_bias = bf16x8{};
-  if (hi == 0) {
-    q_bias[0] = (__bf16)1.0f;
-    q_bias[1] = (__bf16)1.0f;
-  }
+  // |q| for the score bound (this lane holds half of the query's features).
+  float q_ss = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q_ss = __builtin_fmaf((float)qf[ks][e], (float)qf[ks][e], q_ss);
+  const float q_norm = __builtin_sqrtf(sum_halves(q_ss));
 
-  // DMA roles: waves 0-3 copy K (1 KB each), waves 4-7 copy V, lanes 0-7 of
-  // wave 0 copy the 128 bytes of bias pairs.  Each lane fetches the global
+  // DMA roles: waves 0-3 copy K (1 KB each), waves 4-7 copy V, lanes 0-8 of
+  // wave 0 copy the 144-byte tile record.  Each lane fetches the global
   // chunk that belongs in its LDS slot under the swizzle.
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
-  const __amdgpu_buffer_rsrc_t prs = make_rsrc(P, p.pair_bytes);
+  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(R, p.rec_bytes);
   const uint32_t k_row = (uint32_t)p.k_sn * 2u, v_row = (uint32_t)p.v_sn * 2u;
   const int slot = (wave & 3) * 64 + lane;  // 16-byte slot within the K or V tile
   const int s_key = slot >> 3, s_pc = slot & 7;
@@ -217,7 +287,7 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       dma16(krs, &T.k[(wave & 3) * 512], k_voff, n0 * k_row);
     else
       dma16(vrs, &T.v[(wave & 3) * 512], v_voff, n0 * v_row);
-    if (wave == 0 && lane < 8) dma16(prs, &T.bias[0], lane * 16, n0 * 4);
+    if (wave == 0 && lane < kRec / 4) dma16(rrs, &T.rec[0], lane * 16, (uint32_t)t * (kRec * 4));
   };
 
   // Per-lane LDS element offsets of the fragment reads (slot-independent).
@@ -226,55 +296,90 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   for (int ks = 0; ks < 4; ++ks) k_off[ks] = l32 * kHD + (k_chunk(l32, 2 * ks + hi) << 3);
   // V^T transpose reads: block db (features 32db..), k-step s, part pp
   // (keys 16s + 8pp + 4hi + 0..3).  Within its 16-lane group this lane is
-  // the source of key offset (lane&15)>>2 and feature quad lane&3.
-  int v_off[2][2][2];
+  // the source of key offset (lane&15)>>2 and feature quad lane&3.  The
+  // swizzle depends on key&3 only, which s and pp leave unchanged, so those
+  // two are constant offsets (1024 s + 512 pp elements) from one base per db.
+  int v_base[2];
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        const int key = 16 * s + 8 * pp + 4 * hi + ((lane & 15) >> 2);
-        const int a = lane & 3;
-        const int ch = db * 4 + ((lane >> 4) & 1) * 2 + (a >> 1);
-        v_off[db][s][pp] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
-      }
+  for (int db = 0; db < 2; ++db) {
+    const int key = 4 * hi + ((lane & 15) >> 2);
+    const int a = lane & 3;
+    const int ch = db * 4 + ((lane >> 4) & 1) * 2 + (a >> 1);
+    v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
+  }
 
-  float m_run = -INFINITY;  // running max in log2 units (moved lazily)
+  float m_run = kMInit;     // softmax offset in log2 units
   float l_run = 0.f;        // this lane's share of the row sum
   f32x16 o_acc[2] = {f32x16{}, f32x16{}};
   const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
+  // Row bound c*(|q| max|k| + max bias/sm_scale) over all keys.
+  const float m_fix = __builtin_fmaf(q_norm, p.bounds[2 * bh], p.bounds[2 * bh + 1]);
 
   // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t,
-  // wait until tile t+1 has landed, synchronise.
-  auto step = [&](const int t, const Tile& T, Tile& Tfree) {
+  // wait until tile t+1 has landed, synchronise.  The offset m is chosen in
+  // one of three ways (kFirst for tile 0, then kFixed or kLazy for the rest
+  // of the wave's rows):
+  //   kFirst  main pass: m = m_fix when tile 0's exact row max certifies
+  //           that m_fix is within kGap of every row max of the wave (m_fix
+  //           >= every score, and the row max >= tile 0's max); then the
+  //           probabilities of the keys that matter, 2^(x-m) with x within
+  //           ~30 of the row max, stay far above fp32's normal range limit
+  //           2^-126, and the remaining tiles need no max at all.  Repair
+  //           pass: m = tile 0's max.
+  //   kFixed  no max, no rescale, no branch.
+  //   kLazy   x <= c*(|q| max|k| + max bias/sm_scale) over the tile; only
+  //           when that bound exceeds m + kTau can 2^(x-m) leave [0, 2^kTau]:
+  //           then take the exact row max and move m where it is above
+  //           m + kTau, rescaling what has been accumulated.
+  constexpr int kFirst = 0, kFixed = 1, kLazy = 2;
+  bool fixed = false;
+  auto step = [&](auto mode, const int t, const Tile& T, Tile& Tfree) {
+    constexpr int MODE = decltype(mode)::value;
     issue(t + kAhead, Tfree);
 
-    // Scores s = q.k + bias/sm_scale (rows 8g + 4hi + j of the 32x32 result).
-    f32x16 sv = f32x16{};
+    // Scores s = q.k + bias/sm_scale: the accumulator (rows 8g + 4hi + j
+    // of the 32x32 result) starts from the keys' bias values.
+    f32x16 sv;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.rec[8 * g + 4 * hi]);
+      sv[4 * g + 0] = bv[0];
+      sv[4 * g + 1] = bv[1];
+      sv[4 * g + 2] = bv[2];
+      sv[4 * g + 3] = bv[3];
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       sv = mfma32x32x16(*reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]), qf[ks], sv);
-    {
-      const uint32_t pair = T.bias[l32];
-      const u32x4 kb = {hi == 0 ? pair : 0u, 0u, 0u, 0u};
-      sv = mfma32x32x16(__builtin_bit_cast(bf16x8, kb), q_bias, sv);
-    }
 
-    float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+    auto tile_max = [&]() {
+      float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
 #pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
-    mx = fmaxf(mx, sv[15]);
-    const float ms = max_halves(mx) * c;
-    const bool need = t == 0 || ms > m_run + kTau;
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
-      // Move m up to this tile's max and rescale what has been accumulated.
-      const float m_new = need ? ms : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-      o_acc[0] *= alpha;
-      o_acc[1] *= alpha;
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
+      mx = fmaxf(mx, sv[15]);
+      return max_halves(mx) * c;
+    };
+    if constexpr (MODE == kFirst) {
+      const float ms = tile_max();
+      if constexpr (LAZY) {
+        m_run = fmaxf(ms, kMInit);
+      } else {
+        fixed = __builtin_amdgcn_ballot_w64(!(m_fix - ms <= kGap)) == 0;
+        m_run = m_fix;
+      }
+    } else if constexpr (MODE == kLazy) {
+      // (One branch level: nested ones make the register allocator copy
+      // the O accumulators on every tile.)
+      const float ub = __builtin_fmaf(q_norm, T.rec[kKT], T.rec[kKT + 1]);
+      if (__builtin_amdgcn_ballot_w64(ub > m_run + kTau) != 0) {
+        const float ms = tile_max();
+        const float m_new = ms > m_run + kTau ? ms : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+        o_acc[0] *= alpha;
+        o_acc[1] *= alpha;
+      }
     }
 
     const float neg_m = -m_run;
@@ -305,9 +410,9 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
       for (int s = 0; s < 2; ++s) {
         typedef short i16x4 __attribute__((ext_vector_type(4)));
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&T.v[v_off[db][s][0]]);
+            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s]);
         const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&T.v[v_off[db][s][1]]);
+            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s + 512]);
         const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
         const bf16x8 vf = {l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
         o_acc[db] = mfma32x32x16(vf, pb[s], o_acc[db]);
@@ -332,17 +437,27 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
     wait_vm<kAhead - 1>();
   tile_barrier();
 
-  // Four steps per trip so every slot is a compile-time LDS object.
-  int t = 0;
-  for (; t + 4 <= ntiles; t += 4) {
-    step(t, ring0, ring3);
-    step(t + 1, ring1, ring0);
-    step(t + 2, ring2, ring1);
-    step(t + 3, ring3, ring2);
+  step(std::integral_constant<int, kFirst>{}, 0, ring0, ring3);
+  // Tiles 1.. four per trip, so every slot is a compile-time LDS object.
+  auto run = [&](auto mode) {
+    int t = 1;
+    for (; t + 4 <= ntiles; t += 4) {
+      step(mode, t, ring1, ring0);
+      step(mode, t + 1, ring2, ring1);
+      step(mode, t + 2, ring3, ring2);
+      step(mode, t + 3, ring0, ring3);
+    }
+    if (t < ntiles) step(mode, t++, ring1, ring0);
+    if (t < ntiles) step(mode, t++, ring2, ring1);
+    if (t < ntiles) step(mode, t++, ring3, ring2);
+  };
+  if constexpr (LAZY) {
+    run(std::integral_constant<int, kLazy>{});
+  } else {
+    run(std::integral_constant<int, kFixed>{});
+    store = fixed;
+    if (lane == 0) flag_row[wave] = fixed ? 0 : 1;
   }
-  if (t < ntiles) step(t++, ring0, ring3);
-  if (t < ntiles) step(t++, ring1, ring0);
-  if (t < ntiles) step(t++, ring2, ring1);
   // Drain the DMAs still in flight before the workgroup can exit.
   wait_vm<0>();
 
@@ -350,7 +465,7 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
   const float l_tot = sum_halves(l_run);
   const float inv = 1.0f / l_tot;
-  if (q_row < p.M) {
+  if (store && q_row < p.M) {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -366,21 +481,16 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   }
 }
 
-// Pair-buffer geometry: one row per (batch, head) that has its own bias.
-struct PairPlan {
-  int64_t rows_b, rows_h, npad;
-  size_t bytes;
-};
-
-PairPlan pair_plan(int64_t B, int64_t H, int64_t N, int bias_kind, int64_t bias_sb,
-                   int64_t bias_sh) {
-  PairPlan pl;
-  const bool none = bias_kind == GPA_BIAS_NONE;
-  pl.rows_b = (none || bias_sb == 0) ? 1 : B;
-  pl.rows_h = (none || bias_sh == 0) ? 1 : H;
-  pl.npad = (N + kKT - 1) / kKT * kKT;
-  pl.bytes = (size_t)(pl.rows_b * pl.rows_h * pl.npad) * sizeof(uint32_t);
-  return pl;
+// Workspace: one row of ntiles tile records per (batch, head), then two
+// floats of row bounds per (batch, head).
+size_t rec_bytes(int64_t B, int64_t H, int64_t N) {
+  const int64_t ntiles = (N + kKT - 1) / kKT;
+  return (size_t)(B * H * ntiles) * kRec * sizeof(float);
+}
+size_t bounds_bytes(int64_t B, int64_t H) { return (size_t)(B * H) * 2 * sizeof(float); }
+size_t attn_ws_bytes(int64_t B, int64_t H, int64_t M, int64_t N) {
+  const int64_t gx = (M + kQPerWG - 1) / kQPerWG;
+  return rec_bytes(B, H, N) + bounds_bytes(B, H) + (size_t)(B * H * gx) * kWaves;
 }
 
 }  // namespace
@@ -388,10 +498,9 @@ PairPlan pair_plan(int64_t B, int64_t H, int64_t N, int bias_kind, int64_t bias_
 
 using namespace gpa;
 
-extern "C" size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t N, int bias_kind,
-                                                   int64_t bias_sb, int64_t bias_sh) {
-  if (B <= 0 || H <= 0 || N <= 0) return 0;
-  return pair_plan(B, H, N, bias_kind, bias_sb, bias_sh).bytes;
+extern "C" size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t N) {
+  if (B <= 0 || H <= 0 || M <= 0 || N <= 0) return 0;
+  return attn_ws_bytes(B, H, M, N);
 }
 
 extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v, const void* bias,
@@ -456,32 +565,45 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
     gpa_set_error("gpa_attn_keybias_bf16: one head's K/V slice exceeds 2 GiB");
     return GPA_E_UNSUPPORTED;
   }
-  const PairPlan pl = pair_plan(B, H, N, bias_kind, bias_sb, bias_sh);
-  if (!workspace || workspace_bytes < pl.bytes || (uintptr_t)workspace % 16) {
+  const size_t ws_need = attn_ws_bytes(B, H, M, N);
+  if (!workspace || workspace_bytes < ws_need || (uintptr_t)workspace % 16) {
     gpa_set_error("gpa_attn_keybias_bf16: 16-byte aligned workspace of %zu bytes required, %zu "
                   "given",
-                  pl.bytes, workspace ? workspace_bytes : (size_t)0);
+                  ws_need, workspace ? workspace_bytes : (size_t)0);
     return GPA_E_WORKSPACE;
   }
   hipStream_t s = (hipStream_t)stream;
+  const int64_t ntiles = (N + kKT - 1) / kKT;
+  const float c = sm_scale * kLog2e;
 
-  PairArgs pa{};
-  pa.bias = bias;
-  pa.pairs = (uint32_t*)workspace;
-  pa.kind = bias_kind;
-  pa.rows_h = (int)pl.rows_h;
-  pa.sb = bias_sb;
-  pa.sh = bias_sh;
-  pa.sn = bias_sn;
-  pa.N = N;
-  pa.npad = pl.npad;
-  pa.total = pl.rows_b * pl.rows_h * pl.npad;
-  pa.mul = 1.0f / sm_scale;
-  hipLaunchKernelGGL(bias_pairs_kernel, dim3((unsigned)((pa.total + 255) / 256)), dim3(256), 0, s,
-                     pa);
+  RecArgs ra{};
+  ra.k = (const uint16_t*)k;
+  ra.bias = bias;
+  ra.recs = (float*)workspace;
+  ra.kind = bias_kind;
+  ra.H = (int)H;
+  ra.k_sb = k_sb; ra.k_sh = k_sh; ra.k_sn = k_sn;
+  ra.sb = bias_sb; ra.sh = bias_sh; ra.sn = bias_sn;
+  ra.N = N;
+  ra.ntiles = ntiles;
+  ra.total_keys = B * H * ntiles * kKT;
+  ra.mul = 1.0f / sm_scale;
+  ra.c = c;
+  hipLaunchKernelGGL(tile_records_kernel, dim3((unsigned)((ra.total_keys + 255) / 256)), dim3(256),
+                     0, s, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_attn_keybias_bf16: bias pre-pass launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("gpa_attn_keybias_bf16: tile-record pre-pass launch failed: %s",
+                  hipGetErrorString(e));
+    return GPA_E_LAUNCH;
+  }
+  float* bounds = (float*)((char*)workspace + rec_bytes(B, H, N));
+  hipLaunchKernelGGL(row_bounds_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s,
+                     (const float*)workspace, bounds, ntiles);
+  e = hipGetLastError();
+  if (e != hipSuccess) {
+    gpa_set_error("gpa_attn_keybias_bf16: row-bound pre-pass launch failed: %s",
+                  hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
 
@@ -489,7 +611,9 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   p.q = (const uint16_t*)q;
   p.k = (const uint16_t*)k;
   p.v = (const uint16_t*)v;
-  p.pairs = (const uint32_t*)workspace;
+  p.recs = (const float*)workspace;
+  p.bounds = bounds;
+  p.flags = (uint8_t*)bounds + bounds_bytes(B, H);
   p.o = (uint16_t*)o;
   p.lse = lse;
   p.H = (int)H;
@@ -499,19 +623,20 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   p.k_sb = k_sb; p.k_sh = k_sh; p.k_sn = k_sn;
   p.v_sb = v_sb; p.v_sh = v_sh; p.v_sn = v_sn;
   p.o_sb = o_sb; p.o_sh = o_sh; p.o_sm = o_sm;
-  p.pairs_sb = pl.rows_b > 1 ? pl.rows_h * pl.npad : 0;
-  p.pairs_sh = pl.rows_h > 1 ? pl.npad : 0;
   p.lse_sb = lse_sb; p.lse_sh = lse_sh;
   p.k_bytes = (uint32_t)(((N - 1) * k_sn + D) * 2);
   p.v_bytes = (uint32_t)(((N - 1) * v_sn + D) * 2);
-  p.pair_bytes = (uint32_t)(pl.npad * sizeof(uint32_t));
-  p.c = sm_scale * kLog2e;
+  p.rec_bytes = (uint32_t)(ntiles * kRec * sizeof(float));
+  p.c = c;
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
-  if (lse)
-    hipLaunchKernelGGL(attn_keybias_kernel<true>, grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL(attn_keybias_kernel<false>, grid, block, 0, s, p);
+  if (lse) {
+    hipLaunchKernelGGL((attn_keybias_kernel<true, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((attn_keybias_kernel<true, true>), grid, block, 0, s, p);
+  } else {
+    hipLaunchKernelGGL((attn_keybias_kernel<false, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((attn_keybias_kernel<false, true>), grid, block, 0, s, p);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("gpa_attn_keybias_bf16: launch failed: %s", hipGetErrorString(e));

@@ -62,7 +62,7 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_size_t, _vp,     # workspace, workspace_bytes, stream
     ]
     lib.gpa_attn_keybias_workspace_bytes.restype = ctypes.c_size_t
-    lib.gpa_attn_keybias_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int, _i64, _i64]
+    lib.gpa_attn_keybias_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.gpa_attn_keybias_bf16.restype = ctypes.c_int
     lib.gpa_attn_keybias_bf16.argtypes = [
         _vp, _vp, _vp,                 # q, k, v
@@ -242,7 +242,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if B == 0 or H == 0 or M == 0:
         return o, lse
     L = lib()
-    ws_bytes = L.gpa_attn_keybias_workspace_bytes(B, H, N, bias_kind, bsb, bsh)
+    ws_bytes = L.gpa_attn_keybias_workspace_bytes(B, H, M, N)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         rc = L.gpa_attn_keybias_bf16(

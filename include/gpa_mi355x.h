@@ -76,12 +76,13 @@ int gpa_sim_argmax_bf16(const void* a, const void* b,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
-/* Bytes of device workspace gpa_attn_keybias_bf16 needs: the padded buffer
- * of per-key bias pairs (one row per batch/head with its own bias; the
- * reference wrapper allocates the same kind of buffer,
- * merging/fused_attention.py:159-160). */
-size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t N, int bias_kind,
-                                        int64_t bias_sb, int64_t bias_sh);
+/* Bytes of device workspace gpa_attn_keybias_bf16 needs: per (batch, head)
+ * one 144-byte record per 32-key tile, holding the keys' bias/sm_scale
+ * (padded past N) and two per-tile maxima the kernel bounds its scores with,
+ * 8 bytes of row maxima, and one flag byte per 32 queries.  The reference
+ * wrapper allocates the analogous padded bias buffer
+ * (merging/fused_attention.py:159-160). */
+size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t N);
 
 /*
  * Attention with a per-key additive bias, head_dim 64.

@@ -96,6 +96,31 @@ def test_increasing_logits_force_rescales(dev):
     assert (lse.cpu() - ref_lse).abs().max().item() < 2e-3
 
 
+@pytest.mark.parametrize("lse", [False, True])
+def test_fixed_and_repaired_rows_mix(dev, lse):
+    """Rows whose score bound |q| max|k| sits far above their scores go
+    through the repair pass (lazily moved offset); their neighbours in the
+    same workgroup keep the fixed offset.  Both must match the reference."""
+    g = torch.Generator().manual_seed(11)
+    M, N = 600, 1000
+    q = torch.randn(1, 2, M, 64, generator=g) * 0.3
+    k = torch.randn(1, 2, N, 64, generator=g) * 0.3
+    k[:, :, :32] *= -1.0                              # tile 0 scores low for the boosted rows
+    boost = torch.zeros(M, dtype=torch.bool)
+    boost[32:64] = True                               # one whole wave of workgroup 0
+    boost[[5, 300, 555]] = True                       # single rows inside other waves
+    q[:, :, boost] = k[:, :, 40:41].expand(-1, -1, int(boost.sum()), -1) * 100.0
+    q, k = q.bfloat16(), k.bfloat16()
+    v = torch.randn(1, 2, N, 64, generator=g).bfloat16()
+    bias = torch.randn(1, 1, 1, N, generator=g)
+    o, l = attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125, True) \
+        if lse else (attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125), None)
+    ref, ref_lse = attention_reference(q, k, v, bias, 0.125)
+    _check(o, ref)
+    if lse:
+        assert (l.cpu() - ref_lse).abs().max().item() < 2e-3
+
+
 def test_replication_identity(dev):
     """Key j repeated c_j times == key j once with bias log c_j."""
     g = torch.Generator().manual_seed(5)

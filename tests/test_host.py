@@ -120,11 +120,13 @@ def test_attn_empty_problem_is_a_no_op():
 
 def test_attn_workspace_bytes():
     lib = _native.lib()
-    # one row of bias pairs per (batch, head), keys padded to whole 32-key tiles
-    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 68_700, 2, 16 * 68_700, 68_700) == 16 * 68_704 * 4
-    # a bias shared by every head, or no bias, needs a single row
-    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 100, 1, 100, 0) == 128 * 4
-    assert lib.gpa_attn_keybias_workspace_bytes(2, 16, 100, 0, 0, 0) == 128 * 4
+    # per (batch, head): one 144-byte record per 32-key tile, 8 bytes of row
+    # bounds, and one flag byte per wave (8 waves per 256 queries)
+    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 274_800, 68_700) == \
+        16 * 2147 * 144 + 16 * 8 + 16 * 1074 * 8
+    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 256, 32) == 6 * 144 + 6 * 8 + 6 * 8
+    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 257, 33) == 6 * 2 * 144 + 6 * 8 + 6 * 16
+    assert lib.gpa_attn_keybias_workspace_bytes(0, 3, 10, 33) == 0
 
 
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
