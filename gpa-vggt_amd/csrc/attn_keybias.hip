@@ -62,9 +62,11 @@
 namespace gpa {
 namespace {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kQPerWG = kWaves * 32;          // 256 queries per workgroup
+constexpr int kBlk = 2;                       // 32-query blocks per wave
+constexpr int kQPerWave = 32 * kBlk;
+constexpr int kQPerWG = kWaves * kQPerWave;   // 256 queries per workgroup
 constexpr int kKT = 32;                       // keys per tile
 constexpr int kHD = 64;                       // head dim
 constexpr int kRing = 4;                      // LDS tile slots
@@ -81,7 +83,7 @@ struct AttnArgs {
   const uint16_t* v;
   const float* recs;      // [B*H][ntiles][kRec] tile records
   const float* bounds;    // [B*H][2] maxima of the records' words 32 and 33
-  uint8_t* flags;         // [B*H][gx][8] per wave: 1 = rows left to the lazy pass
+  uint8_t* flags;         // [B*H][gx][kWaves] per wave: 1 = rows left to the repair pass
   uint16_t* o;
   float* lse;
   int H;
@@ -226,7 +228,7 @@ __device__ __forceinline__ void tile_barrier() {
 // exit at once; the others recompute their rows with the lazily moved
 // offset, and the flagged waves store theirs.
 template <bool LSE, bool LAZY>
-__global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
+__global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
   // Four separate LDS objects (not one array) so the compiler's LDS-DMA
   // tracking can tell which slot a DMA writes and which a read reads.
   __shared__ Tile ring0, ring1, ring2, ring3;
@@ -240,11 +242,11 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
   bool store = true;
   if constexpr (LAZY) {
-    const uint64_t f = *reinterpret_cast<const uint64_t*>(flag_row);
+    const uint32_t f = *reinterpret_cast<const uint32_t*>(flag_row);
     if (f == 0) return;  // workgroup-uniform: before any barrier or DMA
     store = ((f >> (8 * wave)) & 0xff) != 0;
   }
-  const int64_t q_row = (int64_t)blockIdx.x * kQPerWG + wave * 32 + l32;
+  const int64_t q_base = (int64_t)blockIdx.x * kQPerWG + wave * kQPerWave + l32;
   const float c = p.c;
 
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
@@ -252,42 +254,51 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
   const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
 
-  // Q^T as the B-operand of S^T = K . Q^T: lane supplies query (lane%32),
-  // features 16*ks + 8*hi .. +8.
-  bf16x8 qf[4];
+  // Q^T as the B-operand of S^T = K . Q^T: in block j the lane supplies
+  // query q_base + 32 j, features 16*ks + 8*hi .. +8.  |q| feeds the bound.
+  bf16x8 qf[kBlk][4];
+  float q_norm[kBlk];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = q_row < p.M ? *reinterpret_cast<const bf16x8*>(Q + q_row * p.q_sm + ks * 16 + hi * 8)
-                         : bf16x8{};
-  // |q| for the score bound (this lane holds half of the query's features).
-  float q_ss = 0.f;
+  for (int j = 0; j < kBlk; ++j) {
+    const int64_t row = q_base + 32 * j;
+    float ss = 0.f;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
+                            : bf16x8{};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q_ss = __builtin_fmaf((float)qf[ks][e], (float)qf[ks][e], q_ss);
-  const float q_norm = __builtin_sqrtf(sum_halves(q_ss));
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)qf[j][ks][e], (float)qf[j][ks][e], ss);
+    }
+    q_norm[j] = __builtin_sqrtf(sum_halves(ss));
+  }
 
-  // DMA roles: waves 0-3 copy K (1 KB each), waves 4-7 copy V, lanes 0-8 of
-  // wave 0 copy the 144-byte tile record.  Each lane fetches the global
-  // chunk that belongs in its LDS slot under the swizzle.
+  // DMA roles: wave w copies the w-th kilobyte of the K tile and of the V
+  // tile (keys 8w..8w+7); lanes 0-8 of wave 0 also copy the 144-byte tile
+  // record.  Each lane fetches the global chunk that belongs in its LDS slot
+  // under the swizzle.
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
   const __amdgpu_buffer_rsrc_t rrs = make_rsrc(R, p.rec_bytes);
   const uint32_t k_row = (uint32_t)p.k_sn * 2u, v_row = (uint32_t)p.v_sn * 2u;
-  const int slot = (wave & 3) * 64 + lane;  // 16-byte slot within the K or V tile
+  const int slot = wave * 64 + lane;  // 16-byte slot within the K or V tile
   const int s_key = slot >> 3, s_pc = slot & 7;
   const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
   const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
-  const bool k_wave = wave < 4;
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
 
   auto issue = [&](int t, Tile& T) {
     const uint32_t n0 = (uint32_t)t * kKT;
-    if (k_wave)
-      dma16(krs, &T.k[(wave & 3) * 512], k_voff, n0 * k_row);
-    else
-      dma16(vrs, &T.v[(wave & 3) * 512], v_voff, n0 * v_row);
+    dma16(krs, &T.k[wave * 512], k_voff, n0 * k_row);
+    dma16(vrs, &T.v[wave * 512], v_voff, n0 * v_row);
     if (wave == 0 && lane < kRec / 4) dma16(rrs, &T.rec[0], lane * 16, (uint32_t)t * (kRec * 4));
+  };
+  // Tile t+1 has landed once only tiles t+2 and t+3 are outstanding: three
+  // DMA instructions per tile on wave 0, two on the others.
+  auto wait_next = [&]() {
+    if (wave == 0)
+      wait_vm<3 * (kAhead - 1)>();
+    else
+      wait_vm<2 * (kAhead - 1)>();
   };
 
   // Per-lane LDS element offsets of the fragment reads (slot-independent).
@@ -308,17 +319,24 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
     v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
   }
 
-  float m_run = kMInit;     // softmax offset in log2 units
-  float l_run = 0.f;        // this lane's share of the row sum
-  f32x16 o_acc[2] = {f32x16{}, f32x16{}};
-  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
+  float m_run[kBlk], l_run[kBlk], m_fix[kBlk];
+  f32x16 o_acc[kBlk][2];
   // Row bound c*(|q| max|k| + max bias/sm_scale) over all keys.
-  const float m_fix = __builtin_fmaf(q_norm, p.bounds[2 * bh], p.bounds[2 * bh + 1]);
+  const float row_k = p.bounds[2 * bh], row_b = p.bounds[2 * bh + 1];
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    m_run[j] = kMInit;
+    l_run[j] = 0.f;
+    o_acc[j][0] = f32x16{};
+    o_acc[j][1] = f32x16{};
+    m_fix[j] = __builtin_fmaf(q_norm[j], row_k, row_b);
+  }
+  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 
-  // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t,
-  // wait until tile t+1 has landed, synchronise.  The offset m is chosen in
-  // one of three ways (kFirst for tile 0, then kFixed or kLazy for the rest
-  // of the wave's rows):
+  // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t for
+  // both query blocks, wait until tile t+1 has landed, synchronise.  The
+  // offset m is chosen in one of three ways (kFirst for tile 0, then kFixed
+  // or kLazy for the rest of the wave's rows):
   //   kFirst  main pass: m = m_fix when tile 0's exact row max certifies
   //           that m_fix is within kGap of every row max of the wave (m_fix
   //           >= every score, and the row max >= tile 0's max); then the
@@ -337,73 +355,28 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
     constexpr int MODE = decltype(mode)::value;
     issue(t + kAhead, Tfree);
 
-    // Scores s = q.k + bias/sm_scale: the accumulator (rows 8g + 4hi + j
-    // of the 32x32 result) starts from the keys' bias values.
-    f32x16 sv;
+    // Scores s = q.k + bias/sm_scale: both blocks' accumulators (rows
+    // 8g + 4hi + i of the 32x32 result) start from the keys' bias values,
+    // and each K fragment serves both blocks.
+    f32x16 bias16;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.rec[8 * g + 4 * hi]);
-      sv[4 * g + 0] = bv[0];
-      sv[4 * g + 1] = bv[1];
-      sv[4 * g + 2] = bv[2];
-      sv[4 * g + 3] = bv[3];
+      bias16[4 * g + 0] = bv[0];
+      bias16[4 * g + 1] = bv[1];
+      bias16[4 * g + 2] = bv[2];
+      bias16[4 * g + 3] = bv[3];
     }
+    f32x16 sv[kBlk];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      sv = mfma32x32x16(*reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]), qf[ks], sv);
-
-    auto tile_max = [&]() {
-      float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]);
 #pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
-      mx = fmaxf(mx, sv[15]);
-      return max_halves(mx) * c;
-    };
-    if constexpr (MODE == kFirst) {
-      const float ms = tile_max();
-      if constexpr (LAZY) {
-        m_run = fmaxf(ms, kMInit);
-      } else {
-        fixed = __builtin_amdgcn_ballot_w64(!(m_fix - ms <= kGap)) == 0;
-        m_run = m_fix;
-      }
-    } else if constexpr (MODE == kLazy) {
-      // (One branch level: nested ones make the register allocator copy
-      // the O accumulators on every tile.)
-      const float ub = __builtin_fmaf(q_norm, T.rec[kKT], T.rec[kKT + 1]);
-      if (__builtin_amdgcn_ballot_w64(ub > m_run + kTau) != 0) {
-        const float ms = tile_max();
-        const float m_new = ms > m_run + kTau ? ms : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-        o_acc[0] *= alpha;
-        o_acc[1] *= alpha;
-      }
+      for (int j = 0; j < kBlk; ++j) sv[j] = mfma32x32x16(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
     }
 
-    const float neg_m = -m_run;
-    bf16x8 pb[2];
-    float lsum = 0.f;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
-        const bf16x2 pv = {(__bf16)p0, (__bf16)p1};
-        pb[half][e] = pv[0];
-        pb[half][e + 1] = pv[1];
-        if (LSE)
-          lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
-        else
-          lsum = __builtin_amdgcn_fdot2_f32_bf16(pv, ones2, lsum, false);
-      }
-    }
-    l_run += lsum;
-
-    // O^T += V^T . P^T; the V^T operand of k-step s covers the keys whose
-    // probabilities this lane holds in its score registers 8s..8s+7.
+    // V^T fragments of this tile, shared by both blocks.
+    bf16x8 vf[2][2];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -414,16 +387,79 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
         const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s + 512]);
         const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
-        const bf16x8 vf = {l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
-        o_acc[db] = mfma32x32x16(vf, pb[s], o_acc[db]);
+        vf[db][s] = bf16x8{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
       }
 
-    // Tile t+1 has landed once only tiles t+2 and t+3 are outstanding: two
-    // DMA instructions per tile on wave 0, one on the others.
-    if (wave == 0)
-      wait_vm<2 * (kAhead - 1)>();
-    else
-      wait_vm<kAhead - 1>();
+    auto tile_max = [&](const f32x16& x) {
+      float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
+      mx = fmaxf(mx, x[15]);
+      return max_halves(mx) * c;
+    };
+    if constexpr (MODE == kFirst) {
+      bool bad = false;
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) {
+        const float ms = tile_max(sv[j]);
+        if constexpr (LAZY) {
+          m_run[j] = fmaxf(ms, kMInit);
+        } else {
+          bad = bad || !(m_fix[j] - ms <= kGap);
+          m_run[j] = m_fix[j];
+        }
+      }
+      if constexpr (!LAZY) fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+    } else if constexpr (MODE == kLazy) {
+      // (One branch level per block: nested ones make the register
+      // allocator copy the O accumulators on every tile.)
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) {
+        const float ub = __builtin_fmaf(q_norm[j], T.rec[kKT], T.rec[kKT + 1]);
+        if (__builtin_amdgcn_ballot_w64(ub > m_run[j] + kTau) != 0) {
+          const float ms = tile_max(sv[j]);
+          const float m_new = ms > m_run[j] + kTau ? ms : m_run[j];
+          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+          m_run[j] = m_new;
+          l_run[j] *= alpha;
+          o_acc[j][0] *= alpha;
+          o_acc[j][1] *= alpha;
+        }
+      }
+    }
+
+    // P = 2^(s*c - m) in bf16, row sums, then O^T += V^T . P^T; the V^T
+    // operand of k-step s covers the keys whose probabilities this lane
+    // holds in its score registers 8s..8s+7.
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const float neg_m = -m_run[j];
+      bf16x8 pb[2];
+      float lsum = 0.f;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e], c, neg_m));
+          const float p1 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e + 1], c, neg_m));
+          const bf16x2 pv = {(__bf16)p0, (__bf16)p1};
+          pb[half][e] = pv[0];
+          pb[half][e + 1] = pv[1];
+          if (LSE)
+            lsum = (half == 0 && e == 0) ? p0 + p1 : lsum + (p0 + p1);
+          else
+            lsum = __builtin_amdgcn_fdot2_f32_bf16(pv, ones2, lsum, false);
+        }
+      }
+      l_run[j] += lsum;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) o_acc[j][db] = mfma32x32x16(vf[db][s], pb[s], o_acc[j][db]);
+    }
+
+    wait_next();
     tile_barrier();
   };
 
@@ -431,10 +467,7 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   issue(0, ring0);
   issue(1, ring1);
   issue(2, ring2);
-  if (wave == 0)
-    wait_vm<2 * (kAhead - 1)>();
-  else
-    wait_vm<kAhead - 1>();
+  wait_next();
   tile_barrier();
 
   step(std::integral_constant<int, kFirst>{}, 0, ring0, ring3);
@@ -461,23 +494,29 @@ __global__ __launch_bounds__(kThreads, 4) void attn_keybias_kernel(AttnArgs p) {
   // Drain the DMAs still in flight before the workgroup can exit.
   wait_vm<0>();
 
-  // Epilogue: combine the two key halves of the row sum, normalise, store.
+  // Epilogue: combine the two key halves of the row sums, normalise, store.
+  if (!store) return;
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
-  const float l_tot = sum_halves(l_run);
-  const float inv = 1.0f / l_tot;
-  if (store && q_row < p.M) {
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+  for (int j = 0; j < kBlk; ++j) {
+    const int64_t row = q_base + 32 * j;
+    const float l_tot = sum_halves(l_run[j]);
+    const float inv = 1.0f / l_tot;
+    if (row < p.M) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = db * 32 + 8 * g + 4 * hi;
-        const bf16x4 ov = {(__bf16)(o_acc[db][4 * g + 0] * inv),
-                           (__bf16)(o_acc[db][4 * g + 1] * inv),
-                           (__bf16)(o_acc[db][4 * g + 2] * inv),
-                           (__bf16)(o_acc[db][4 * g + 3] * inv)};
-        *reinterpret_cast<bf16x4*>(O + q_row * p.o_sm + d0) = ov;
-      }
-    if (p.lse && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q_row] = m_run + __log2f(l_tot);
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = db * 32 + 8 * g + 4 * hi;
+          const bf16x4 ov = {(__bf16)(o_acc[j][db][4 * g + 0] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 1] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 2] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 3] * inv)};
+          *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
+        }
+      if (p.lse && hi == 0)
+        p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_run[j] + __log2f(l_tot);
+    }
   }
 }
 
