@@ -13,7 +13,6 @@ kernels and their caller (noheat61/GPA-VGGT):
                  fp64 closed form              (pins the above)
   merge.py       token_merge_bipartite2d       merging/merge.py:39-256
                  fp64 brute-force K/V mean     (pins merge.heads)
-  workloads.py   seeded synthetic inputs for the benchmark configurations
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
 `bench.py` may import it, and only as the checker or the timed CPU baseline.
