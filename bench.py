@@ -29,6 +29,7 @@ for _p in (str(REPO), str(REPO / "gpa-vggt_amd")):
         sys.path.insert(0, _p)
 
 PEAK_BF16_TFLOPS = 2516.6     # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+HBM_BYTES_PER_S = 8.0e12      # MI355X HBM3E
 SM_SCALE = 64 ** -0.5
 TRAFFIC_FILE = REPO / "profiles" / "attn_keybias_traffic.json"
 
@@ -199,6 +200,19 @@ def main(argv=None) -> int:
             kernels[f"attn_keybias_200f_{tag}_16h_274800x{nk}"] = kernel_entry(
                 W.attn_flops(16, 274_800, nk, 64), t)
             del q2, k2, v2, b2
+        # Row f1: the deterministic K/V merge at the 200-frame shape (all
+        # 207,955 source tokens merged into 66,845 slots), K fp32 and V bf16.
+        from merging import _native
+        for dt, tag, elem in ((torch.float32, "k_f32", 4), (torch.bfloat16, "v_bf16", 2)):
+            t3, off3, tok3 = W.merge_inputs(m=274_800, n=66_845, dtype=dt, seed=3, device=dev)
+            fn = lambda: _native.merge_heads(t3, off3, tok3, 66_845, True)  # noqa: E731
+            fn()
+            t = statistics.median(event_ms(fn, 5))
+            nbytes = W.merge_bytes(274_800, 66_845, 16, 64, elem)
+            kernels[f"merge_heads_200f_{tag}_16h_274800to66845"] = {
+                "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+                "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+            del t3, off3, tok3
         log("[bench] 200-frame shapes done")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12

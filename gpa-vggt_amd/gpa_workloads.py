@@ -16,6 +16,9 @@ Shapes follow a VGGT-1B aggregator at 518x518: 1374 tokens per frame
                          bf16 and per-key bias log(c), c the counts of a
                          uniform multinomial assignment of M tokens to N keys
                          with every key given at least one.
+  merge_inputs           a K/V merge of the same shape: [1,H,M,64] rows and
+                         the slot lists (offsets, tokens) of a random
+                         assignment of M tokens to N slots with those counts.
 """
 from __future__ import annotations
 
@@ -110,3 +113,22 @@ def attn_flops(bh: int, m: int, n: int, d: int = HEAD_DIM) -> float:
 def sim_flops(b: int, m: int, n: int, d: int) -> float:
     """Algorithmic FLOPs of one similarity-argmax call."""
     return 2.0 * b * m * n * d
+
+
+def merge_inputs(m: int = 274_800, n: int = 66_845, heads: int = HEADS, d: int = HEAD_DIM,
+                 dtype=torch.float32, seed: int = 0, device="cpu"):
+    """(t [1,H,m,d], offsets [n+1] int64, tokens [m] int64): every token in
+    exactly one of n slot lists, list lengths from `merge_counts`."""
+    g = _gen(device, seed + 11)
+    t = torch.randn(1, heads, m, d, generator=g, device=device).to(dtype)
+    counts = merge_counts(m, n, seed=seed, device=device).to(torch.int64)
+    offsets = torch.zeros(n + 1, dtype=torch.int64, device=device)
+    offsets[1:] = torch.cumsum(counts, 0)
+    tokens = torch.randperm(m, generator=g, device=device)
+    return t, offsets, tokens
+
+
+def merge_bytes(m: int, n: int, heads: int, d: int, elem: int) -> int:
+    """Algorithmic HBM bytes of one merge: every row read once, every slot
+    written once, the lists read once."""
+    return (m + n) * heads * d * elem + 8 * (m + n + 1)

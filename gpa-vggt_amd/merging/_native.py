@@ -9,8 +9,10 @@ two custom ops:
     gpa::sim_argmax(Tensor a, Tensor b) -> (Tensor max_f32, Tensor idx_i64)
     gpa::attn_keybias(Tensor q, Tensor k, Tensor v, Tensor? bias,
                       float sm_scale, bool return_lse) -> (Tensor o, Tensor lse)
+    gpa::merge_heads(Tensor t, Tensor offsets, Tensor tokens, int slots,
+                     bool mean) -> (Tensor out, Tensor size, Tensor log_size)
 
-Both launch on torch's current stream of the input's device.  There is no
+All launch on torch's current stream of the input's device.  There is no
 fallback: a missing library or a non-GPU tensor raises.
 """
 from __future__ import annotations
@@ -23,7 +25,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -34,6 +36,12 @@ GPA_E_LAUNCH = -4
 GPA_BIAS_NONE = 0
 GPA_BIAS_F32 = 1
 GPA_BIAS_BF16 = 2
+
+GPA_DTYPE_F32 = 0
+GPA_DTYPE_BF16 = 1
+GPA_DTYPE_F16 = 2
+GPA_MERGE_SUM = 0
+GPA_MERGE_MEAN = 1
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -78,6 +86,15 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_size_t,          # workspace, workspace_bytes
         ctypes.c_float, _vp,           # sm_scale, stream
     ]
+    lib.gpa_merge_heads.restype = ctypes.c_int
+    lib.gpa_merge_heads.argtypes = [
+        _vp, ctypes.c_int, _vp,        # t, dtype, out
+        _vp, _vp,                      # offsets, tokens
+        _i64, _i64, _i64, _i64, _i64,  # B, H, N, S, D
+        _i64, _i64, _i64,              # t strides (b, h, n)
+        _i64, _i64, _i64,              # out strides (b, h, s)
+        ctypes.c_int, _vp, _vp, _vp,   # mode, size_out, log_size_out, stream
+    ]
 
 
 def lib() -> ctypes.CDLL:
@@ -103,7 +120,8 @@ def lib() -> ctypes.CDLL:
 
 def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
-            "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16")
+            "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
+            "gpa_merge_heads")
 
 
 def _check(rc: int, what: str) -> None:
@@ -146,7 +164,7 @@ def _rows_ok(t: torch.Tensor, align_elems: int) -> bool:
     """Unit inner stride, other strides multiples of `align_elems`, aligned base."""
     if t.stride(-1) != 1:
         return False
-    if t.data_ptr() % (2 * align_elems) != 0:
+    if t.data_ptr() % (t.element_size() * align_elems) != 0:
         return False
     return all(s % align_elems == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
 
@@ -265,3 +283,53 @@ def _attn_keybias_fake(q, k, v, bias, sm_scale, return_lse):
     o = q.new_empty(B, H, M, D, dtype=torch.bfloat16)
     lse = q.new_empty((B, H, M) if return_lse else (0,), dtype=torch.float32)
     return o, lse
+
+
+_MERGE_DTYPES = {torch.float32: GPA_DTYPE_F32, torch.bfloat16: GPA_DTYPE_BF16,
+                 torch.float16: GPA_DTYPE_F16}
+
+
+@torch.library.custom_op("gpa::merge_heads", mutates_args=())
+def merge_heads(t: torch.Tensor, offsets: torch.Tensor, tokens: torch.Tensor, slots: int,
+                mean: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Segmented sum / mean of t [B, H, N, D] rows over per-slot token lists.
+
+    offsets [B*slots + 1] and tokens [B*N] (int64, positions within a batch
+    element) list every output slot's tokens; returns out [B, H, slots, D]
+    in t's dtype, the list lengths [B, slots] and their logs (fp32).
+    """
+    dev = _require_gpu(t, offsets, tokens)
+    if t.dim() != 4:
+        raise ValueError(f"gpa::merge_heads: t must be [B,H,N,D], got {tuple(t.shape)}")
+    if t.dtype not in _MERGE_DTYPES:
+        raise NotImplementedError(f"gpa::merge_heads: dtype {t.dtype} not supported")
+    if offsets.dtype != torch.int64 or tokens.dtype != torch.int64:
+        raise ValueError("gpa::merge_heads: offsets and tokens must be int64")
+    B, H, N, D = t.shape
+    if offsets.numel() != B * slots + 1 or tokens.numel() != B * N:
+        raise ValueError(f"gpa::merge_heads: offsets {offsets.numel()} / tokens {tokens.numel()} "
+                         f"do not match B={B}, slots={slots}, N={N}")
+    offsets, tokens = offsets.contiguous(), tokens.contiguous()
+    out = torch.empty(B, H, slots, D, device=dev, dtype=t.dtype)
+    size = torch.empty(B, slots, device=dev, dtype=torch.float32)
+    log_size = torch.empty(B, slots, device=dev, dtype=torch.float32)
+    if B == 0 or slots == 0:
+        return out, size, log_size
+    if not _rows_ok(t, 16 // t.element_size()):
+        t = t.contiguous()
+    with torch.cuda.device(dev):
+        rc = lib().gpa_merge_heads(
+            t.data_ptr(), _MERGE_DTYPES[t.dtype], out.data_ptr(),
+            offsets.data_ptr(), tokens.data_ptr(), B, H, N, slots, D,
+            _st(t, 0), _st(t, 1), _rs(t, 2), _st(out, 0), _st(out, 1), _rs(out, 2),
+            GPA_MERGE_MEAN if mean else GPA_MERGE_SUM, size.data_ptr(), log_size.data_ptr(),
+            _stream(dev))
+    _check(rc, "gpa::merge_heads")
+    return out, size, log_size
+
+
+@merge_heads.register_fake
+def _merge_heads_fake(t, offsets, tokens, slots, mean):
+    B, H, N, D = t.shape
+    return (t.new_empty(B, H, slots, D), t.new_empty(B, slots, dtype=torch.float32),
+            t.new_empty(B, slots, dtype=torch.float32))

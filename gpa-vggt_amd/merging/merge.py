@@ -13,6 +13,14 @@ Orderings the reference leaves to torch's sort are fixed here:
     source position -- a stable descending sort.
 These are the orders torch's GPU radix sort produces for such inputs.
 `merge.index` exposes the index tensors for inspection.
+
+`merge` and `merge.heads` in "sum" / "mean" mode (fp32, bf16, fp16 rows)
+run the deterministic gfx950 merge kernel (`gpa::merge_heads`): every
+output slot lists its own token and the tokens merged into it once per
+merge, and the sum runs over that list in fp32 in a fixed order.  The
+reference's scatter_reduce_ (reference :246-249) sums with atomics in a
+run-dependent order, in the rows' own precision; other modes keep that
+gather + scatter_reduce_ on the device.
 """
 from __future__ import annotations
 
@@ -21,6 +29,7 @@ from typing import Callable, Optional
 
 import torch
 
+from . import _native
 from .fused_similarity import fused_similarity_argmax
 
 __all__ = ["token_merge_bipartite2d", "PROJ_SEED", "dst_mask", "num_dst_tokens"]
@@ -151,8 +160,40 @@ def token_merge_bipartite2d(
         size[:, unm_len:].scatter_add_(1, dst_slot, torch.ones(B, r, device=dev,
                                                                 dtype=torch.float32))
 
+        # Token list of every output slot, for the deterministic merge
+        # kernel: slot i < unm_len holds kept source token unm_abs[i]; dst
+        # slot unm_len + j holds dst token b_pos[j] first, then the source
+        # tokens merged into it in increasing position.  Every input token
+        # appears exactly once, so each batch element lists N tokens.
+        slots = unm_len + num_dst
+        key = torch.cat([torch.arange(unm_len, device=dev).expand(B, unm_len),
+                         (unm_len + torch.arange(num_dst, device=dev)).expand(B, num_dst),
+                         unm_len + dst_slot], dim=1)
+        tok = torch.cat([unm_abs, b_pos.expand(B, num_dst), src_abs], dim=1)
+        sub = torch.cat([torch.zeros(B, unm_len + num_dst, device=dev, dtype=torch.int64),
+                         src_abs + 1], dim=1)      # the slot's own token sorts first
+        order = torch.argsort(key * (N + 1) + sub, dim=1)
+        csr_tokens = torch.gather(tok, 1, order).reshape(-1)
+        csr_offsets = torch.zeros(B * slots + 1, device=dev, dtype=torch.int64)
+        csr_offsets[1:] = torch.cumsum(size.reshape(-1).to(torch.int64), 0)
+
+    def kernel_merge(t: torch.Tensor, mode: str) -> Optional[torch.Tensor]:
+        """The deterministic gfx950 merge for sum / mean of fp32, bf16 and
+        fp16 rows that split into 16-byte runs; None when it does not apply."""
+        if (mode not in ("mean", "sum") or t.dtype not in (torch.float32, torch.bfloat16,
+                                                           torch.float16)
+                or t.shape[-1] % (16 // t.element_size()) != 0 or not t.is_cuda):
+            return None
+        out, _, _ = _native.merge_heads(t, csr_offsets, csr_tokens, slots, mode == "mean")
+        return out
+
     def merge(x: torch.Tensor, mode: str = "mean") -> torch.Tensor:
         """[B, N, C] -> [B, unm_len + num_dst, C]: unmerged src, then dst."""
+        if x.shape[0] != B or x.shape[1] != N:
+            raise ValueError("merge input does not match the merge mapping")
+        out = kernel_merge(x.unsqueeze(1), mode)
+        if out is not None:
+            return out.squeeze(1)
         nb, _, c = x.shape
         out = torch.empty(nb, unm_len + num_dst, c, device=x.device, dtype=x.dtype)
         torch.gather(x, 1, unm_abs[..., None].expand(nb, unm_len, c), out=out[:, :unm_len])
@@ -167,6 +208,9 @@ def token_merge_bipartite2d(
         nb, nh, ntok, d = t.shape
         if nb != B or ntok != N:
             raise ValueError("merge_heads input does not match the merge mapping")
+        out = kernel_merge(t, mode)
+        if out is not None:
+            return out
         out = torch.empty(nb, nh, unm_len + num_dst, d, device=t.device, dtype=t.dtype)
         torch.gather(t, 2, unm_abs[:, None, :, None].expand(nb, nh, unm_len, d),
                      out=out[:, :, :unm_len])
@@ -182,5 +226,6 @@ def token_merge_bipartite2d(
     merge.index = SimpleNamespace(
         a_idx=a_pos, b_idx=b_pos, node_max=node_max, node_idx=node_idx, edge_idx=edge,
         dst_idx=dst_slot, unm_abs_idx=unm_abs, src_abs_idx=src_abs,
-        num_dst=num_dst, num_src=num_src, r=r, unm_len=unm_len, mask=mask)
+        num_dst=num_dst, num_src=num_src, r=r, unm_len=unm_len, mask=mask,
+        slot_offsets=csr_offsets, slot_tokens=csr_tokens)
     return merge

@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Two kernels sit behind this boundary:
+ * Three kernels sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -10,6 +10,9 @@
  *   gpa_attn_keybias_bf16 — flash attention with a per-key additive bias
  *                           (replaces merging/fused_attention.py:130-180,
  *                            the Triton `_attn_keybias_kernel` at :70-127).
+ *   gpa_merge_heads       — deterministic segmented mean/sum of token rows,
+ *                           the K/V merge (replaces the scatter_reduce_ of
+ *                           merging/merge.py:234-250).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -33,7 +36,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 2
+#define GPA_ABI_VERSION 3
 
 enum {
   GPA_OK = 0,
@@ -45,6 +48,10 @@ enum {
 
 /* Bias element types accepted by gpa_attn_keybias_bf16. */
 enum { GPA_BIAS_NONE = 0, GPA_BIAS_F32 = 1, GPA_BIAS_BF16 = 2 };
+
+/* Element types and reductions of gpa_merge_heads. */
+enum { GPA_DTYPE_F32 = 0, GPA_DTYPE_BF16 = 1, GPA_DTYPE_F16 = 2 };
+enum { GPA_MERGE_SUM = 0, GPA_MERGE_MEAN = 1 };
 
 /* ABI version of the loaded library (GPA_ABI_VERSION at build time). */
 int gpa_abi_version(void);
@@ -109,6 +116,29 @@ int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
                           int64_t lse_sb, int64_t lse_sh,
                           void* workspace, size_t workspace_bytes,
                           float sm_scale, void* stream);
+
+/*
+ * Deterministic segmented reduction of token rows: the K/V merge.
+ *   out[b,h,s,:] = reduce over n in tokens[offsets[b*S+s] .. offsets[b*S+s+1])
+ *                  of t[b,h,n,:]                  (GPA_MERGE_SUM or GPA_MERGE_MEAN)
+ * fp32 accumulation in list order, one rounding to `dtype` (t and out share
+ * it).  Token values are positions in [0, N) of batch b; every slot's list is
+ * its own token followed by the tokens merged into it.  size_out /
+ * log_size_out (nullable, fp32 [B*S]) receive the list lengths and their
+ * natural logs.  Out-of-range tokens or offsets make that slot NaN (no
+ * out-of-bounds access).  Rows: unit feature stride, 16-byte aligned; D a
+ * multiple of 4 (fp32) or 8 (bf16, fp16).
+ * Replaces merging/merge.py:234-250 (`merge.heads`, and `merge` with H = 1),
+ * whose scatter_reduce_ sums in a run-dependent order, and the size of
+ * merging/merge.py:211-217 with the log-count bias of
+ * vggt/layers/attention.py:250-260.
+ */
+int gpa_merge_heads(const void* t, int dtype, void* out,
+                    const int64_t* offsets, const int64_t* tokens,
+                    int64_t B, int64_t H, int64_t N, int64_t S, int64_t D,
+                    int64_t t_sb, int64_t t_sh, int64_t t_sn,
+                    int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                    int mode, float* size_out, float* log_size_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -129,6 +129,34 @@ def test_attn_workspace_bytes():
     assert lib.gpa_attn_keybias_workspace_bytes(0, 3, 10, 33) == 0
 
 
+def _merge(**kw):
+    args = dict(t=FAKE, dtype=0, out=FAKE, offsets=FAKE, tokens=FAKE, B=1, H=2, N=10, S=4, D=64,
+                tsb=1280, tsh=640, tsn=64, osb=512, osh=256, osn=64, mode=1, size=None,
+                log_size=None, stream=None)
+    args.update(kw)
+    return _native.lib().gpa_merge_heads(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(N=-1), _native.GPA_E_INVALID),
+    (dict(offsets=None), _native.GPA_E_INVALID),
+    (dict(mode=5), _native.GPA_E_INVALID),
+    (dict(dtype=9), _native.GPA_E_INVALID),
+    (dict(D=62, tsn=62, osn=62), _native.GPA_E_INVALID),     # D not a multiple of 4
+    (dict(tsn=66), _native.GPA_E_INVALID),                   # misaligned row stride
+    (dict(t=FAKE + 4), _native.GPA_E_INVALID),               # misaligned base (fp32)
+    (dict(B=1 << 20, S=1 << 12), _native.GPA_E_UNSUPPORTED),
+])
+def test_merge_argument_errors(kw, code):
+    assert _merge(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_merge_empty_is_a_no_op():
+    assert _merge(B=0) == _native.GPA_OK
+    assert _merge(S=0) == _native.GPA_OK
+
+
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
     (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
     (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
