@@ -213,6 +213,40 @@ def main(argv=None) -> int:
                 "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
                 "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
             del t3, off3, tok3
+        # Row f2: the frame-special split path at 200 frames: own-frame
+        # attention (200 frames x 16 heads, 1374 queries x 1369 keys, LSE),
+        # shared-set attention (274,800 queries x 6,000 keys with the pooled
+        # log-size bias, LSE), and the LSE combine into [1, 274800, 1024].
+        from merging.fused_attention import combine_by_lse
+        S, P, pts, npool = 200, 1374, 5, 25
+        qf = (torch.randn(S, 16, P, 64, device=dev) / 8).bfloat16()
+        kf = (torch.randn(S, 16, P - pts, 64, device=dev) / 8).bfloat16()
+        vf = (torch.randn(S, 16, P - pts, 64, device=dev) / 8).bfloat16()
+        fn = lambda: attention_keybias(qf, kf, vf, None, SM_SCALE, return_lse=True)  # noqa: E731
+        out_a, lse_a = fn()
+        t = statistics.median(event_ms(fn, 5))
+        kernels["attn_frame_own_3200bh_1374x1369"] = kernel_entry(W.attn_flops(S * 16, P, P - pts, 64), t)
+        del kf, vf
+        qs = qf.view(1, S, 16, P, 64).permute(0, 2, 1, 3, 4).reshape(1, 16, S * P, 64)
+        del qf
+        ks = (torch.randn(1, 16, S * (pts + npool), 64, device=dev) / 8).bfloat16()
+        vs = (torch.randn(1, 16, S * (pts + npool), 64, device=dev) / 8).bfloat16()
+        bs = torch.zeros(1, 16, 1, S * (pts + npool), device=dev)
+        bs[..., S * pts:] = torch.randint(1, 12, (1, 16, 1, S * npool), device=dev).float().log()
+        bs = bs.bfloat16()
+        fn = lambda: attention_keybias(qs, ks, vs, bs, SM_SCALE, return_lse=True)  # noqa: E731
+        out_b, lse_b = fn()
+        t = statistics.median(event_ms(fn, 5))
+        kernels["attn_frame_shared_16h_274800x6000"] = kernel_entry(
+            W.attn_flops(16, S * P, S * (pts + npool), 64), t)
+        fn = lambda: combine_by_lse(out_a, lse_a, out_b, lse_b, S)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 5))
+        nbytes = 3 * S * P * 16 * 64 * 2 + 2 * S * P * 16 * 4
+        kernels["lse_combine_200f_16h_274800"] = {
+            "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+        del qs, ks, vs, bs, out_a, lse_a, out_b, lse_b
         log("[bench] 200-frame shapes done")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12

@@ -11,6 +11,8 @@ two custom ops:
                       float sm_scale, bool return_lse) -> (Tensor o, Tensor lse)
     gpa::merge_heads(Tensor t, Tensor offsets, Tensor tokens, int slots,
                      bool mean) -> (Tensor out, Tensor size, Tensor log_size)
+    gpa::lse_combine(Tensor out_a, Tensor lse_a, Tensor out_b, Tensor lse_b,
+                     int frames) -> Tensor y
 
 All launch on torch's current stream of the input's device.  There is no
 fallback: a missing library or a non-GPU tensor raises.
@@ -86,6 +88,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_size_t,          # workspace, workspace_bytes
         ctypes.c_float, _vp,           # sm_scale, stream
     ]
+    lib.gpa_lse_combine_bf16.restype = ctypes.c_int
+    lib.gpa_lse_combine_bf16.argtypes = [_vp] * 5 + [_i64] * 5 + [_i64] * 16 + [_i64] * 3 + [_vp]
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -121,7 +125,7 @@ def lib() -> ctypes.CDLL:
 def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
-            "gpa_merge_heads")
+            "gpa_merge_heads", "gpa_lse_combine_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -333,3 +337,57 @@ def _merge_heads_fake(t, offsets, tokens, slots, mean):
     B, H, N, D = t.shape
     return (t.new_empty(B, H, slots, D), t.new_empty(B, slots, dtype=torch.float32),
             t.new_empty(B, slots, dtype=torch.float32))
+
+
+@torch.library.custom_op("gpa::lse_combine", mutates_args=())
+def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
+                lse_b: torch.Tensor, frames: int) -> torch.Tensor:
+    """Merge the own-frame attention (out_a [B*S, H, P, D], lse_a [B*S, H, P])
+    and the shared-set attention (out_b [B, H, S*P, D], lse_b [B, H, S*P]) by
+    their log2 LSE; returns y [B, S*P, H*D] bf16."""
+    dev = _require_gpu(out_a, lse_a, out_b, lse_b)
+    for name, t in (("out_a", out_a), ("out_b", out_b)):
+        if t.dtype != torch.bfloat16 or t.dim() != 4:
+            raise ValueError(f"gpa::lse_combine: {name} must be bf16 [.,H,.,D], got "
+                             f"{t.dtype} {tuple(t.shape)}")
+    for name, t in (("lse_a", lse_a), ("lse_b", lse_b)):
+        if t.dtype != torch.float32 or t.dim() != 3:
+            raise ValueError(f"gpa::lse_combine: {name} must be fp32 [.,H,.], got "
+                             f"{t.dtype} {tuple(t.shape)}")
+    S = int(frames)
+    BS, H, P, D = out_a.shape
+    B, Hb, N, Db = out_b.shape
+    if S <= 0 or BS != B * S or Hb != H or Db != D or N != S * P or \
+            tuple(lse_a.shape) != (BS, H, P) or tuple(lse_b.shape) != (B, H, N):
+        raise ValueError(f"gpa::lse_combine: shapes do not match: out_a {tuple(out_a.shape)}, "
+                         f"lse_a {tuple(lse_a.shape)}, out_b {tuple(out_b.shape)}, "
+                         f"lse_b {tuple(lse_b.shape)}, frames {frames}")
+    if not _rows_ok(out_a, 8):
+        out_a = out_a.contiguous()
+    if not _rows_ok(out_b, 8):
+        out_b = out_b.contiguous()
+    y = torch.empty(B, N, H * D, device=dev, dtype=torch.bfloat16)
+    if y.numel() == 0:
+        return y
+    sa0, sa1, sa2 = out_a.stride()[:3]
+    la0, la1, la2 = lse_a.stride()
+    sb0, sb1, sb2 = out_b.stride()[:3]
+    lb0, lb1, lb2 = lse_b.stride()
+    with torch.cuda.device(dev):
+        rc = lib().gpa_lse_combine_bf16(
+            out_a.data_ptr(), lse_a.data_ptr(), out_b.data_ptr(), lse_b.data_ptr(), y.data_ptr(),
+            B, H, N, P, D,
+            S * sa0, sa1, sa0, sa2,            # out_a (b, h, s, p)
+            S * la0, la1, la0, la2,            # lse_a
+            sb0, sb1, P * sb2, sb2,            # out_b (b, h, s, p), token n = s*P + p
+            lb0, lb1, P * lb2, lb2,            # lse_b
+            y.stride(0), y.stride(1), D,       # y (b, n, h)
+            _stream(dev))
+    _check(rc, "gpa::lse_combine")
+    return y
+
+
+@lse_combine.register_fake
+def _lse_combine_fake(out_a, lse_a, out_b, lse_b, frames):
+    B, H, N, D = out_b.shape
+    return out_b.new_empty(B, N, H * D, dtype=torch.bfloat16)

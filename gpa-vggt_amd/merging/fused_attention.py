@@ -10,7 +10,8 @@ Math matches SDPA(q, k, v, attn_mask=bias): scores = q@k^T * scale + bias,
 softmax over keys in fp32, P rounded to bf16 for the P@V product, fp32
 accumulation.  With return_lse the log2 softmax denominators come back as
 well, so callers can split the key set and recombine exactly
-(reference :123-127).
+(reference :123-127); `combine_by_lse` is that recombination for the
+frame-special split path of vggt/layers/attention.py:148-176.
 """
 from __future__ import annotations
 
@@ -18,7 +19,7 @@ import torch
 
 from . import _native  # noqa: F401  (registers torch.ops.gpa.*)
 
-__all__ = ["attention_keybias", "LOG2E"]
+__all__ = ["attention_keybias", "combine_by_lse", "LOG2E"]
 
 LOG2E = 1.4426950408889634
 
@@ -51,3 +52,18 @@ def attention_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     k = k.to(q.dtype)
     o, lse = torch.ops.gpa.attn_keybias(q, k, v, bias, float(sm_scale), bool(return_lse))
     return (o, lse) if return_lse else o
+
+
+def combine_by_lse(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
+                   lse_b: torch.Tensor, frames: int) -> torch.Tensor:
+    """Merge the two halves of the frame-special split attention.
+
+    out_a [B*S, H, P, D], lse_a [B*S, H, P]: attention of every frame's P
+    queries over the frame's own keys (frame-major, as the own-frame call of
+    vggt/layers/attention.py:157 returns it); out_b [B, H, S*P, D], lse_b
+    [B, H, S*P]: attention of all queries over the shared keys (:162).  The
+    log2 LSEs weight the two (:166-176); returns [B, S*P, H*D] in bf16, the
+    layout the output projection takes.  The weights and the sum are fp32
+    (the reference rounds the weights to the activation dtype first).
+    """
+    return torch.ops.gpa.lse_combine(out_a, lse_a, out_b, lse_b, int(frames))

@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Three kernels sit behind this boundary:
+ * Four kernels sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -13,6 +13,8 @@
  *   gpa_merge_heads       — deterministic segmented mean/sum of token rows,
  *                           the K/V merge (replaces the scatter_reduce_ of
  *                           merging/merge.py:234-250).
+ *   gpa_lse_combine_bf16  — merge of two partial attentions by their log2
+ *                           LSE (replaces vggt/layers/attention.py:166-176).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -139,6 +141,27 @@ int gpa_merge_heads(const void* t, int dtype, void* out,
                     int64_t t_sb, int64_t t_sh, int64_t t_sn,
                     int64_t o_sb, int64_t o_sh, int64_t o_sn,
                     int mode, float* size_out, float* log_size_out, void* stream);
+
+/*
+ * Merge of two attentions over a partition of the keys by their log2 LSE,
+ * written in the token-major projection layout:
+ *   m = max(la, lb), wa = 2^(la-m), wb = 2^(lb-m)
+ *   y[b, n, h*D + d] = (oa[b,h,n,d]*wa + ob[b,h,n,d]*wb) / (wa + wb)     (fp32, bf16 out)
+ * Every operand is addressed per (b, h, s, p) with token n = s*P + p (element
+ * strides *_b, *_h, *_s, *_p), so the own-frame output [B*S, H, P, D] and the
+ * shared-set output [B, H, N, D] are both plain strides; y has strides
+ * (y_b, y_n, y_h) and unit feature stride.  N must be a multiple of P,
+ * D a multiple of 8, rows 16-byte aligned.
+ * Replaces the combine of the frame-special split path,
+ * vggt/layers/attention.py:166-176 (with the final transpose to [B, N, C]).
+ */
+int gpa_lse_combine_bf16(const void* oa, const float* la, const void* ob, const float* lb,
+                         void* y, int64_t B, int64_t H, int64_t N, int64_t P, int64_t D,
+                         int64_t oa_b, int64_t oa_h, int64_t oa_s, int64_t oa_p,
+                         int64_t la_b, int64_t la_h, int64_t la_s, int64_t la_p,
+                         int64_t ob_b, int64_t ob_h, int64_t ob_s, int64_t ob_p,
+                         int64_t lb_b, int64_t lb_h, int64_t lb_s, int64_t lb_p,
+                         int64_t y_b, int64_t y_n, int64_t y_h, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2,7 +2,10 @@
 
 Bar (bf16 output vs the fp32 reference on the same bf16 inputs):
 max-abs <= 2e-2 and mean-abs <= 5e-3, plus a tighter internal bound
-(mean-abs <= 2e-3) with sharp, N(0,1)-scaled logits; log2 LSE within 2e-3.
+(mean-abs <= 2e-3) with sharp, N(0,1)-scaled logits.  The kernel's log2 LSE
+sums the bf16-rounded probabilities the P.V product uses; each term is
+within 2^-8 relative of the fp32 one (8 significant bits), so the LSE is
+within 2^-8 / ln 2 < 5.7e-3 of the reference's fp32 sum (LSE_TOL).
 """
 import math
 
@@ -17,6 +20,7 @@ from oracle.attention import attention_reference, lse_combine
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS = 2e-2, 5e-3
+LSE_TOL = 2.0 ** -8 / 0.6931471805599453 + 1e-5
 
 
 def _inputs(B, H, M, N, seed, qk_scale=0.5, bias="bf16"):
@@ -56,18 +60,16 @@ def test_matches_fp32_reference(dev, B, H, M, N, bias):
     assert lse.shape == (B, H, M) and lse.dtype == torch.float32
     ref, ref_lse = attention_reference(q, k, v, b, 0.125)
     _check(o, ref)
-    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-3
+    assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
 
 
 def test_output_without_lse_matches(dev):
-    """Without the LSE the row sum is taken over the bf16 P (on the matrix
-    core), with it over the fp32 P: the outputs agree to bf16 rounding."""
+    """Asking for the LSE changes nothing else: the outputs are identical."""
     q, k, v, b = _inputs(1, 2, 200, 300, seed=1)
     args = (q.to(dev), k.to(dev), v.to(dev), b.to(dev), 0.125)
     o1 = attention_keybias(*args)
     o2, _ = attention_keybias(*args, return_lse=True)
-    err = (o1.float() - o2.float()).abs()
-    assert err.max().item() < 2e-2 and err.mean().item() < 1e-3
+    assert torch.equal(o1, o2)
 
 
 def test_sharp_logits_and_large_bias(dev):
@@ -78,7 +80,7 @@ def test_sharp_logits_and_large_bias(dev):
     o, lse = attention_keybias(q.to(dev), k.to(dev), v.to(dev), b.to(dev), 0.125, True)
     ref, ref_lse = attention_reference(q, k, v, b, 0.125)
     _check(o, ref)
-    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-3
+    assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
 
 
 def test_increasing_logits_force_rescales(dev):
@@ -93,7 +95,7 @@ def test_increasing_logits_force_rescales(dev):
     o, lse = attention_keybias(q.to(dev), k.to(dev), v.to(dev), None, 4.0, True)
     ref, ref_lse = attention_reference(q, k, v, None, 4.0)
     _check(o, ref)
-    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-3
+    assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
 
 
 @pytest.mark.parametrize("lse", [False, True])
@@ -118,7 +120,7 @@ def test_fixed_and_repaired_rows_mix(dev, lse):
     ref, ref_lse = attention_reference(q, k, v, bias, 0.125)
     _check(o, ref)
     if lse:
-        assert (l.cpu() - ref_lse).abs().max().item() < 2e-3
+        assert (l.cpu() - ref_lse).abs().max().item() < LSE_TOL
 
 
 def test_replication_identity(dev):
