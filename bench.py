@@ -7,9 +7,11 @@ workload (16 heads, 274,800 queries, 68,700 merged keys, head_dim 64), both
 on synthetic inputs already resident in HBM.  `value` is the step's
 algorithmic TFLOP/s (2*M*N*D for the similarity, 4*BH*M*N*D for attention).
 The JSON line also carries per-kernel ms / TFLOP/s / % of the bf16 dense
-MFMA peak, the reference 200-frame shapes, the roofline of the dominant
-kernel and a CPU baseline (the torch restatement of the reference path, timed
-on a bounded sample on this host).
+MFMA peak, the reference 200-frame shapes, the end-to-end latency of one GPA
+block (100 frames) and of the whole GPA aggregator (200 frames) on the
+random-init VGGT-1B harness, the roofline of the dominant kernel and a CPU
+baseline (the torch restatement of the reference path, timed on a bounded
+sample on this host).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -47,7 +49,77 @@ def parse_args(argv=None):
     ap.add_argument("--no-200f", action="store_true", help="skip the 200-frame shape sweep")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
                     help="seconds of CPU work per baseline leg (similarity, attention)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the GPA block (100 frames) and aggregator (200 frames) latencies")
     return ap.parse_args(argv)
+
+
+def e2e_latency(dev) -> dict:
+    """End-to-end latencies on the random-init VGGT-1B aggregator harness.
+
+    * GPA block: one merged global block (LayerNorm -> QKV -> projected
+      similarity-argmax -> K/V merge -> biased attention -> proj -> MLP) on
+      100 frames x 1374 tokens from shifted-texture images;
+    * aggregator: the full stack (DINOv2 ViT-L/14 patch embed, 24 frame + 24
+      global blocks on the GPA schedule) on 200 frames of 518 x 518 images,
+      with the reference defaults, and with the variant of 64 pooled patch
+      summaries per frame in the shared set (pool stride 5) and every merged
+      block at 25 % keep (no core blocks).
+    Timing follows eval/bench_e2e.py: 2 warm-up calls, mean of 3.
+    """
+    import torch
+    import gpa_aggregator as A
+
+    res = {}
+    bf16 = torch.bfloat16
+
+    def run(fn):
+        def call():
+            with torch.no_grad(), torch.autocast("cuda", dtype=bf16):
+                return fn()
+        return call
+
+    cfg = A.GpaConfig()
+    model = A.build_aggregator(cfg, device=dev)
+    frames = 100
+    imgs = A.shifted_texture_images(frames, device=dev).to(bf16)
+    with torch.no_grad(), torch.autocast("cuda", dtype=bf16):
+        tokens = model.embed(imgs).reshape(1, frames * cfg.tokens_per_frame, cfg.embed_dim)
+    _, _, cos, sin = model.rope_tables(frames, dev)
+    blk = model.global_blocks[9]
+    ms, peak = A.timed(run(lambda: blk(tokens, (cos, sin), 9)))
+    res["gpa_block_100f"] = {
+        "ms": round(ms, 2), "peak_gib": round(peak, 2),
+        "workload": "merged global block 9 (ratio 0.98): 137,400 tokens -> 33,945 merged keys"}
+    del tokens, imgs, cos, sin
+    log(f"[bench] GPA block 100 frames: {ms:.1f} ms")
+
+    frames = 200
+    imgs = A.shifted_texture_images(frames, device=dev).to(bf16)
+    variants = (("reference_defaults", cfg, model),
+                ("pool64_keep25", A.GpaConfig(broadcast_pool=5, core_blocks=()), None))
+    for tag, c, m in variants:
+        if m is None:
+            m = A.build_aggregator(c, device=dev)
+        ms, peak = A.timed(run(lambda: m(imgs)))
+        tracer = A.StageTimer()
+        m.set_tracer(tracer)
+        tracer.start()
+        run(lambda: m(imgs))()
+        stages = tracer.totals()
+        m.set_tracer(None)
+        flops = A.aggregator_flops(c, frames)
+        res[f"aggregator_200f_{tag}"] = {
+            "ms": round(ms, 1), "peak_gib": round(peak, 2),
+            "stages_ms": {k: round(v, 2) for k, v in sorted(stages.items(), key=lambda kv: -kv[1])},
+            "tflop": {k: round(v / 1e12, 2) for k, v in flops.items()},
+            "schedule": {"early_frame_split": c.early_frame_split, "broadcast_pool": c.broadcast_pool,
+                         "merge": [c.merging, c.merge_end, c.merge_ratio],
+                         "core_blocks": list(c.core_blocks), "core_merge_ratio": c.core_merge_ratio}}
+        log(f"[bench] aggregator 200 frames ({tag}): {ms:.1f} ms")
+        del m
+        torch.cuda.empty_cache()
+    return res
 
 
 def event_ms(fn, reps: int):
@@ -261,6 +333,13 @@ def main(argv=None) -> int:
                 "traffic": traffic, "kernel": "attn_keybias_kernel",
                 "flops_per_launch": f_attn}
 
+    e2e = None
+    if not args.no_e2e:
+        del q, k, v, bias
+        torch.cuda.empty_cache()
+        e2e = e2e_latency(dev)
+        q, k, v, bias = W.attn_inputs(m=274_800, n=68_700, seed=0, device=dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline ...")
@@ -285,6 +364,7 @@ def main(argv=None) -> int:
                                 "x 274800 queries x 68700 merged keys x d64 (200 frames x 1374 tokens)"),
                    "sm_scale": SM_SCALE, "bias": "log(count), bf16, [1,16,1,N]"},
         "kernels": kernels,
+        "e2e": e2e,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -1,0 +1,550 @@
+"""GPA aggregator harness: a random-init VGGT-1B aggregator with the GPA block
+schedule, running the merging package's gfx950 kernels, for end-to-end latency.
+
+This is the measurement harness around the hot path, not a model port.  It
+restates, in plain torch modules, the layer sequence whose latency the
+merging kernels sit in:
+
+  * DINOv2 ViT-L/14 with 4 registers as the patch embedder
+    (vggt/layers/vision_transformer.py:57-310; 24 blocks, LayerNorm eps 1e-6,
+    LayerScale 1.0, plain attention over each frame's 1374 tokens);
+  * camera + register tokens prepended per frame, 2D RoPE positions with the
+    special tokens at 0 (vggt/models/aggregator.py:249-291);
+  * 24 frame blocks alternating with 24 global blocks
+    (aggregator.py:299-347), pre-LN blocks with LayerScale 0.01
+    (vggt/layers/block.py:84-96), qk LayerNorm and RoPE (frequency 100,
+    vggt/layers/rope.py:167-209);
+  * the GPA schedule of aggregator.py:133-150 and :317-325: global blocks
+    below `early_frame_split` run frame attention plus the shared K/V set
+    (vggt/layers/attention.py:73-176, split path), global blocks in
+    [merging, merge_end] merge K/V (attention.py:233-268) at `merge_ratio`,
+    the core blocks at `core_merge_ratio`.
+
+Everything on the merging path goes through the drop-in package:
+`token_merge_bipartite2d` (similarity-argmax kernel + deterministic merge
+kernel), `attention_keybias` (biased flash attention), `combine_by_lse`.
+Frame attention (no bias) runs the same attention kernel with bias=None by
+default; `frame_attn="sdpa"` switches the plain frame attention to torch's
+SDPA, the reference's choice at attention.py:270-276, for comparison.
+
+Weights are random (no checkpoint is available offline): Linear weights
+N(0, 0.02^2), biases 0, LayerNorm weight 1 / bias 0, LayerScale gammas at the
+reference's init values.  Run under `torch.autocast("cuda", bf16)` on a
+bf16 model, as eval/bench_e2e.py:76-92 does.
+
+Known departure: RoPE angles are computed in fp32 (cos/sin of p * f);
+the reference builds them through an einsum that autocast may run in bf16.
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from merging.fused_attention import attention_keybias, combine_by_lse
+from merging.merge import token_merge_bipartite2d
+
+RESNET_MEAN = (0.485, 0.456, 0.406)
+RESNET_STD = (0.229, 0.224, 0.225)
+MERGE_GENERATOR_SEED = 33              # attention.py:238-239
+
+
+@dataclass
+class GpaConfig:
+    """Aggregator shape and GPA schedule; defaults are the paper's
+    (aggregator.py:53-79, eval/eval_co3d.py:100-123)."""
+    img_size: int = 518
+    patch_size: int = 14
+    embed_dim: int = 1024
+    depth: int = 24
+    num_heads: int = 16
+    mlp_ratio: float = 4.0
+    num_register_tokens: int = 4
+    rope_freq: float = 100.0
+    init_values: float = 0.01
+    merging: Optional[int] = 9
+    merge_end: int = 23
+    merge_ratio: float = 0.98
+    early_frame_split: int = 9
+    broadcast_pool: int = 8
+    core_blocks: Tuple[int, ...] = (13, 14, 15, 16)
+    core_merge_ratio: float = 0.2
+    merge_metric_dim: int = 128
+    merge_grid: int = 2
+    frame_attn: str = "gpa"            # "gpa" (attention kernel, bias=None) or "sdpa"
+    vit_depth: int = 24                # DINOv2 ViT-L/14 blocks
+    dpt_blocks: Tuple[int, ...] = (4, 11, 17, 23)   # outputs kept (aggregator.py:296)
+
+    @property
+    def grid(self) -> int:
+        return self.img_size // self.patch_size
+
+    @property
+    def num_special(self) -> int:
+        return 1 + self.num_register_tokens
+
+    @property
+    def tokens_per_frame(self) -> int:
+        return self.grid * self.grid + self.num_special
+
+    def global_merging(self, block: int) -> Optional[int]:
+        """The block index if global block `block` merges K/V (aggregator.py:317-325)."""
+        if self.merging is None:
+            return None
+        in_window = (block >= self.merging
+                     and (self.merge_end < 0 or block <= self.merge_end)
+                     and block >= self.early_frame_split
+                     and (block not in self.core_blocks or self.core_merge_ratio > 0))
+        return block if in_window else None
+
+    def block_kind(self, block: int) -> str:
+        """'frame_special', 'merged' or 'global' for global block `block`."""
+        if block < min(self.early_frame_split, self.depth):
+            return "frame_special"
+        return "merged" if self.global_merging(block) is not None else "global"
+
+    def block_merge_ratio(self, block: int) -> float:
+        return self.core_merge_ratio if block in self.core_blocks else self.merge_ratio
+
+
+def vanilla_config(**kw) -> GpaConfig:
+    """VGGT without GPA: plain global attention everywhere (eval_co3d.py:127-128)."""
+    return GpaConfig(merging=None, early_frame_split=0, **kw)
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+# ---------------------------------------------------------------------------
+
+class Rope2D:
+    """2D rotary embedding: the first half of each head's features rotates
+    with the row coordinate, the second half with the column coordinate, each
+    half as [x1, x2] -> [x1 cos - x2 sin, x2 cos + x1 sin] with frequencies
+    freq^(-2i/half) (rope.py:92-209)."""
+
+    def __init__(self, freq: float):
+        self.freq = freq
+
+    def tables(self, pos: torch.Tensor, head_dim: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """pos [T, 2] int -> (cos, sin) [T, head_dim] fp32."""
+        half = head_dim // 2
+        inv = self.freq ** (-torch.arange(0, half, 2, dtype=torch.float64,
+                                          device=pos.device) / half)
+        ang = pos.to(torch.float64)[..., None] * inv               # [T, 2, half/2]
+        ang = torch.cat((ang, ang), dim=-1).reshape(pos.shape[0], head_dim)
+        return ang.cos().float(), ang.sin().float()
+
+    @staticmethod
+    def apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """x [..., T, D] (any float dtype), cos/sin [T, D] -> rotated x."""
+        d = x.shape[-1]
+        xr = x.unflatten(-1, (2, 2, d // 4))
+        rot = torch.stack((-xr[..., 1, :], xr[..., 0, :]), dim=-2).flatten(-3)
+        return x * cos.to(x.dtype) + rot * sin.to(x.dtype)
+
+
+class LayerScale(nn.Module):
+    def __init__(self, dim: int, init: float):
+        super().__init__()
+        self.gamma = nn.Parameter(torch.full((dim,), float(init)))
+
+    def forward(self, x):
+        return x * self.gamma
+
+
+class Mlp(nn.Module):
+    def __init__(self, dim: int, hidden: int):
+        super().__init__()
+        self.fc1 = nn.Linear(dim, hidden)
+        self.fc2 = nn.Linear(hidden, dim)
+
+    def forward(self, x):
+        return self.fc2(F.gelu(self.fc1(x)))
+
+
+def _frame_attention(q, k, v, scale: float, backend: str) -> torch.Tensor:
+    """Plain attention, [b, H, T, D] -> [b, H, T, D] bf16."""
+    if backend == "sdpa":
+        return F.scaled_dot_product_attention(q, k, v)
+    return attention_keybias(q, k, v, None, scale)
+
+
+class GpaAttention(nn.Module):
+    """Attention of a VGGT block with the GPA global paths (attention.py:17-282)."""
+
+    def __init__(self, dim: int, heads: int, qk_norm: bool, norm_eps: float, cfg: GpaConfig):
+        super().__init__()
+        self.heads, self.head_dim = heads, dim // heads
+        self.scale = self.head_dim ** -0.5
+        self.qkv = nn.Linear(dim, 3 * dim)
+        self.q_norm = nn.LayerNorm(self.head_dim, eps=norm_eps) if qk_norm else nn.Identity()
+        self.k_norm = nn.LayerNorm(self.head_dim, eps=norm_eps) if qk_norm else nn.Identity()
+        self.proj = nn.Linear(dim, dim)
+        self.cfg = cfg
+        self.frame_special = False
+        self.merge_ratio = cfg.merge_ratio
+        self.tracer: Optional["StageTimer"] = None
+
+    def _mark(self, name: str) -> None:
+        if self.tracer is not None:
+            self.tracer.mark(name)
+
+    def forward(self, x: torch.Tensor, rope_cs=None, global_merging: Optional[int] = None):
+        B, N, C = x.shape
+        H, D = self.heads, self.head_dim
+        qkv = self.qkv(x).view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv.unbind(0)
+        q, k = self.q_norm(q), self.k_norm(k)
+        if rope_cs is not None:
+            cos, sin = rope_cs
+            q, k = Rope2D.apply(q, cos, sin), Rope2D.apply(k, cos, sin)
+        self._mark("qkv")
+
+        if self.frame_special:
+            out = self._frame_special(q, k, v, B, N, C)
+            self._mark("frame_special_attn")
+            return self.proj(out)
+
+        if global_merging is not None:
+            gen = torch.Generator(device=x.device)
+            gen.manual_seed(MERGE_GENERATOR_SEED)
+            r = int(N * self.merge_ratio)
+            g = self.cfg.grid
+            m = token_merge_bipartite2d(x, g, g, self.cfg.merge_grid, self.cfg.merge_grid, r,
+                                        False, gen, metric_dim=self.cfg.merge_metric_dim,
+                                        num_special=self.cfg.num_special)
+            k = m.heads(k, "mean")
+            v = m.heads(v, "mean")
+            bias = m.size.reshape(B, 1, 1, -1).log().to(q.dtype).expand(B, H, 1, k.shape[2])
+            self._mark("merge")
+            out = attention_keybias(q, k, v, bias, self.scale)
+            self._mark("merged_attn")
+        elif N > self.cfg.tokens_per_frame:
+            out = attention_keybias(q, k, v, None, self.scale)
+            self._mark("global_attn")
+        else:
+            out = _frame_attention(q, k, v, self.scale, self.cfg.frame_attn)
+            self._mark("frame_attn")
+        return self.proj(out.transpose(1, 2).reshape(B, N, C))
+
+    def _frame_special(self, q, k, v, B, N, C) -> torch.Tensor:
+        """Frame attention + shared K/V set, split path (attention.py:148-176)."""
+        if q.dtype == torch.float32:
+            dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") \
+                else torch.bfloat16
+            q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        H, D = self.heads, self.head_dim
+        pts, g = self.cfg.num_special, self.cfg.grid
+        P = g * g + pts
+        S = N // P
+        if S * P != N:
+            raise ValueError(f"frame_special: {N} tokens is not a multiple of {P}")
+        q_f = q.view(B, H, S, P, D).permute(0, 2, 1, 3, 4).reshape(B * S, H, P, D)
+        k5, v5 = k.view(B, H, S, P, D), v.view(B, H, S, P, D)
+        own_k = k5[:, :, :, pts:].permute(0, 2, 1, 3, 4).reshape(B * S, H, P - pts, D)
+        own_v = v5[:, :, :, pts:].permute(0, 2, 1, 3, 4).reshape(B * S, H, P - pts, D)
+        out_a, lse_a = attention_keybias(q_f, own_k, own_v, None, self.scale, return_lse=True)
+        del own_k, own_v
+        kp = self.cfg.broadcast_pool
+        if kp > 0:
+            pooled_k, pooled_v, pool_size, _ = pool_shared(k5, v5, pts, g, kp)
+            sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
+            sh_v = torch.cat([v5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_v], dim=2)
+            bias = torch.zeros(B, H, 1, sh_k.shape[2], device=q.device, dtype=torch.float32)
+            bias[:, :, 0, S * pts:] = pool_size.log().reshape(B, H, -1)
+            bias = bias.to(q.dtype)
+        else:
+            sh_k = k5[:, :, :, :pts].reshape(B, H, S * pts, D)
+            sh_v = v5[:, :, :, :pts].reshape(B, H, S * pts, D)
+            bias = None
+        self._mark("pool")
+        out_b, lse_b = attention_keybias(q, sh_k, sh_v, bias, self.scale, return_lse=True)
+        return combine_by_lse(out_a, lse_a, out_b, lse_b, S)
+
+
+def pool_shared(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid: int, kp: int):
+    """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140).
+
+    k5/v5 [B, H, S, P, D].  Seeds are the stride-kp lattice patches; every
+    patch joins the seed whose key it matches best by cosine (per head), and
+    a summary is the mean of its group, for keys and values alike.  Returns
+    (pooled_k, pooled_v [B, H, S*npool, D] in the input dtype, size
+    [B, H, S, npool] fp32, assign [B, H, S, grid*grid] int64).
+    """
+    B, H, S, P, D = k5.shape
+    nh = -(-grid // kp)
+    npool = nh * nh
+    xk = k5[:, :, :, pts:].reshape(B, H, S, grid, grid, D)
+    seeds = xk[:, :, :, ::kp, ::kp].reshape(B, H, S, npool, D).float()
+    a = xk.reshape(B, H, S, grid * grid, D).float()
+    a = a / a.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    seeds = seeds / seeds.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    assign = torch.matmul(a, seeds.transpose(-1, -2).contiguous()).argmax(-1)
+    del a, seeds
+    size = torch.zeros(B, H, S, npool, device=k5.device, dtype=torch.float32)
+    size.scatter_add_(3, assign, torch.ones_like(assign, dtype=torch.float32))
+    idx = assign[..., None].expand(B, H, S, grid * grid, D)
+    out = []
+    for t5 in (k5, v5):
+        acc = torch.zeros(B, H, S, npool, D, device=k5.device, dtype=torch.float32)
+        acc.scatter_add_(3, idx, t5[:, :, :, pts:].reshape(B, H, S, grid * grid, D).float())
+        acc /= size.clamp_min(1.0).unsqueeze(-1)
+        out.append(acc.reshape(B, H, S * npool, D).to(t5.dtype))
+    return out[0], out[1], size, assign
+
+
+class Block(nn.Module):
+    """Pre-LN transformer block with LayerScale (block.py:84-96)."""
+
+    def __init__(self, dim: int, heads: int, mlp_ratio: float, ls_init: float,
+                 qk_norm: bool, norm_eps: float, cfg: GpaConfig):
+        super().__init__()
+        self.norm1 = nn.LayerNorm(dim, eps=norm_eps)
+        self.attn = GpaAttention(dim, heads, qk_norm, 1e-5, cfg)
+        self.ls1 = LayerScale(dim, ls_init)
+        self.norm2 = nn.LayerNorm(dim, eps=norm_eps)
+        self.mlp = Mlp(dim, int(dim * mlp_ratio))
+        self.ls2 = LayerScale(dim, ls_init)
+
+    def forward(self, x, rope_cs=None, global_merging=None):
+        x = x + self.ls1(self.attn(self.norm1(x), rope_cs, global_merging))
+        return x + self.ls2(self.mlp(self.norm2(x)))
+
+
+class DinoV2Reg(nn.Module):
+    """DINOv2 ViT-L/14 with register tokens as the patch embedder
+    (vision_transformer.py:259-310): conv patchify, cls + position
+    embedding, registers after cls, 24 blocks, final LayerNorm; returns the
+    normalised patch tokens."""
+
+    def __init__(self, cfg: GpaConfig):
+        super().__init__()
+        dim = cfg.embed_dim
+        self.patch = nn.Conv2d(3, dim, cfg.patch_size, cfg.patch_size)
+        self.cls_token = nn.Parameter(torch.zeros(1, 1, dim))
+        self.pos_embed = nn.Parameter(torch.zeros(1, cfg.grid * cfg.grid + 1, dim))
+        self.register_tokens = nn.Parameter(torch.zeros(1, cfg.num_register_tokens, dim))
+        self.blocks = nn.ModuleList(
+            Block(dim, cfg.num_heads, cfg.mlp_ratio, 1.0, False, 1e-6, cfg)
+            for _ in range(cfg.vit_depth))
+        self.norm = nn.LayerNorm(dim, eps=1e-6)
+        self.nreg = cfg.num_register_tokens
+
+    def forward(self, img: torch.Tensor) -> torch.Tensor:
+        x = self.patch(img).flatten(2).transpose(1, 2)
+        x = torch.cat((self.cls_token.expand(x.shape[0], -1, -1).to(x.dtype), x), dim=1)
+        x = x + self.pos_embed.to(x.dtype)
+        x = torch.cat((x[:, :1], self.register_tokens.expand(x.shape[0], -1, -1).to(x.dtype),
+                       x[:, 1:]), dim=1)
+        for blk in self.blocks:
+            x = blk(x)
+        return self.norm(x)[:, 1 + self.nreg:]
+
+
+class StageTimer:
+    """Device-time marks on the current stream, summed per stage name."""
+
+    def __init__(self):
+        self.events: List[Tuple[str, torch.cuda.Event]] = []
+
+    def start(self) -> None:
+        self.events = []
+        self.mark("start")
+
+    def mark(self, name: str) -> None:
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.events.append((name, e))
+
+    def totals(self) -> Dict[str, float]:
+        torch.cuda.synchronize()
+        out: Dict[str, float] = {}
+        for (_, e0), (name, e1) in zip(self.events, self.events[1:]):
+            out[name] = out.get(name, 0.0) + e0.elapsed_time(e1)
+        return out
+
+
+class GpaAggregator(nn.Module):
+    """The VGGT aggregator with the GPA schedule (aggregator.py:26-357)."""
+
+    def __init__(self, cfg: GpaConfig):
+        super().__init__()
+        self.cfg = cfg
+        dim = cfg.embed_dim
+        self.patch_embed = DinoV2Reg(cfg)
+        self.camera_token = nn.Parameter(torch.randn(1, 2, 1, dim) * 1e-6)
+        self.register_token = nn.Parameter(torch.randn(1, 2, cfg.num_register_tokens, dim) * 1e-6)
+        mk = lambda: Block(dim, cfg.num_heads, cfg.mlp_ratio, cfg.init_values, True, 1e-5, cfg)  # noqa: E731
+        self.frame_blocks = nn.ModuleList(mk() for _ in range(cfg.depth))
+        self.global_blocks = nn.ModuleList(mk() for _ in range(cfg.depth))
+        for i, blk in enumerate(self.global_blocks):
+            blk.attn.frame_special = cfg.block_kind(i) == "frame_special"
+            blk.attn.merge_ratio = cfg.block_merge_ratio(i)
+        self.rope = Rope2D(cfg.rope_freq)
+        self.register_buffer("mean", torch.tensor(RESNET_MEAN).view(1, 1, 3, 1, 1), persistent=False)
+        self.register_buffer("std", torch.tensor(RESNET_STD).view(1, 1, 3, 1, 1), persistent=False)
+        self.tracer: Optional[StageTimer] = None
+
+    def set_tracer(self, tracer: Optional[StageTimer]) -> None:
+        self.tracer = tracer
+        for blk in list(self.frame_blocks) + list(self.global_blocks):
+            blk.attn.tracer = tracer
+
+    def _mark(self, name: str) -> None:
+        if self.tracer is not None:
+            self.tracer.mark(name)
+
+    def positions(self, device) -> torch.Tensor:
+        return frame_positions(self.cfg.grid, self.cfg.num_special, device)
+
+    def embed(self, images: torch.Tensor) -> torch.Tensor:
+        """[B, S, 3, H, W] in [0, 1] -> tokens [B*S, P, C] in the model dtype."""
+        B, S, C_in, Hh, Ww = images.shape
+        dt = self.camera_token.dtype
+        x = ((images - self.mean) / self.std).to(dt).view(B * S, C_in, Hh, Ww)
+        patches = self.patch_embed(x).to(dt)
+        cam = _first_vs_rest(self.camera_token, B, S)
+        reg = _first_vs_rest(self.register_token, B, S)
+        return torch.cat((cam, reg, patches), dim=1).to(dt)
+
+    def rope_tables(self, frames: int, device):
+        cos, sin = self.rope.tables(self.positions(device), self.cfg.embed_dim // self.cfg.num_heads)
+        return cos, sin, cos.repeat(frames, 1), sin.repeat(frames, 1)
+
+    def forward(self, images: torch.Tensor) -> List[torch.Tensor]:
+        B, S = images.shape[:2]
+        tokens = self.embed(images)
+        self._mark("patch_embed")
+        P, C = tokens.shape[1], tokens.shape[2]
+        cos_f, sin_f, cos_g, sin_g = self.rope_tables(S, images.device)
+        outputs = []
+        for i in range(self.cfg.depth):
+            tokens = self.frame_blocks[i](tokens.view(B * S, P, C), (cos_f, sin_f))
+            self._mark("frame_block")
+            frame_out = tokens.view(B, S, P, C)
+            tokens = self.global_blocks[i](tokens.view(B, S * P, C), (cos_g, sin_g),
+                                           self.cfg.global_merging(i))
+            self._mark(f"global_block_{self.cfg.block_kind(i)}")
+            if i in self.cfg.dpt_blocks:
+                outputs.append(torch.cat((frame_out, tokens.view(B, S, P, C)), dim=-1))
+        return outputs
+
+
+def frame_positions(grid: int, num_special: int, device="cpu") -> torch.Tensor:
+    """[P, 2] RoPE positions of one frame: specials at (0, 0), patch (y, x)
+    at (y + 1, x + 1), row-major (aggregator.py:279-288, rope.py:54-65)."""
+    yx = torch.cartesian_prod(torch.arange(grid, device=device), torch.arange(grid, device=device))
+    return torch.cat((torch.zeros(num_special, 2, dtype=yx.dtype, device=device), yx + 1))
+
+
+def _first_vs_rest(tok: torch.Tensor, B: int, S: int) -> torch.Tensor:
+    """(1, 2, X, C) -> (B*S, X, C): slot 0 for frame 0, slot 1 for the others
+    (aggregator.py:420-442)."""
+    first = tok[:, :1].expand(B, 1, *tok.shape[2:])
+    rest = tok[:, 1:].expand(B, S - 1, *tok.shape[2:])
+    return torch.cat((first, rest), dim=1).reshape(B * S, *tok.shape[2:])
+
+
+def init_random_(model: nn.Module, seed: int = 0) -> nn.Module:
+    """Random init in place: Linear/Conv weights N(0, 0.02^2), biases 0,
+    LayerNorm 1/0, position embedding N(0, 0.02^2); LayerScale and the
+    special tokens keep their constructor values."""
+    g = torch.Generator(device=next(model.parameters()).device)
+    g.manual_seed(seed)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, (nn.Linear, nn.Conv2d)):
+                mod.weight.normal_(0.0, 0.02, generator=g)
+                if mod.bias is not None:
+                    mod.bias.zero_()
+            elif isinstance(mod, nn.LayerNorm):
+                mod.weight.fill_(1.0)
+                mod.bias.zero_()
+            elif isinstance(mod, DinoV2Reg):
+                mod.pos_embed.normal_(0.0, 0.02, generator=g)
+                mod.cls_token.normal_(0.0, 1e-6, generator=g)
+                mod.register_tokens.normal_(0.0, 1e-6, generator=g)
+    return model
+
+
+def build_aggregator(cfg: Optional[GpaConfig] = None, device="cuda", dtype=torch.bfloat16,
+                     seed: int = 0) -> GpaAggregator:
+    """A random-init aggregator on `device` in `dtype`, in eval mode."""
+    cfg = cfg or GpaConfig()
+    with torch.device(device):
+        model = GpaAggregator(cfg)
+    init_random_(model, seed)
+    return model.to(dtype).eval()
+
+
+def shifted_texture_images(frames: int, size: int = 518, shift: int = 64, seed: int = 0,
+                           device="cpu", dtype=torch.float32) -> torch.Tensor:
+    """[1, frames, 3, size, size] i.i.d. U[0,1] RGB crops of one shared random
+    texture at per-frame random offsets in [0, shift)^2: every frame is a
+    translated view of the same content."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    tex = torch.rand(3, size + shift, size + shift, generator=g, device=device)
+    off = torch.randint(0, shift, (frames, 2), generator=g, device=device).tolist()
+    imgs = torch.stack([tex[:, y:y + size, x:x + size] for y, x in off])
+    return imgs.unsqueeze(0).to(dtype)
+
+
+def timed(fn, warmup: int = 2, iters: int = 3) -> Tuple[float, float]:
+    """(mean ms, peak GiB) with the protocol of eval/bench_e2e.py:49-71:
+    warm-up calls, synchronize, reset the peak, `iters` calls, synchronize."""
+    out = None
+    for _ in range(warmup):
+        out = fn()
+    torch.cuda.synchronize()
+    del out
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    out = None
+    for _ in range(iters):
+        del out
+        out = fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / iters * 1e3
+    peak = torch.cuda.max_memory_allocated() / 2 ** 30
+    del out
+    torch.cuda.empty_cache()
+    return ms, peak
+
+
+def aggregator_flops(cfg: GpaConfig, frames: int) -> Dict[str, float]:
+    """Algorithmic FLOPs of one aggregator forward, by part (dense GEMMs,
+    attention contractions, similarity); elementwise work is not counted."""
+    C, P, Hd = cfg.embed_dim, cfg.tokens_per_frame, cfg.embed_dim // cfg.num_heads
+    T = frames * P
+    hid = int(C * cfg.mlp_ratio)
+    dense_block = 2.0 * T * (3 * C * C + C * C + 2 * C * hid)
+    frame_attn = 4.0 * frames * cfg.num_heads * P * P * Hd
+    out = {"dense": dense_block * (cfg.vit_depth + 2 * cfg.depth)
+           + 2.0 * frames * cfg.grid ** 2 * 3 * cfg.patch_size ** 2 * C,
+           "frame_attn": frame_attn * (cfg.vit_depth + cfg.depth),
+           "global_attn": 0.0, "similarity": 0.0}
+    pts, g = cfg.num_special, cfg.grid
+    from merging.merge import num_dst_tokens
+    for i in range(cfg.depth):
+        kind = cfg.block_kind(i)
+        if kind == "frame_special":
+            npool = (-(-g // cfg.broadcast_pool)) ** 2 if cfg.broadcast_pool > 0 else 0
+            out["global_attn"] += 4.0 * frames * cfg.num_heads * P * (P - pts) * Hd
+            out["global_attn"] += 4.0 * cfg.num_heads * T * frames * (pts + npool) * Hd
+        elif kind == "merged":
+            nd = num_dst_tokens(frames, g, g, cfg.merge_grid, cfg.merge_grid, pts, False)
+            ns = T - nd
+            r = min(ns, int(T * cfg.block_merge_ratio(i)))
+            out["global_attn"] += 4.0 * cfg.num_heads * T * (T - r) * Hd
+            out["similarity"] += 2.0 * ns * nd * cfg.merge_metric_dim
+            out["dense"] += 2.0 * T * C * cfg.merge_metric_dim
+        else:
+            out["global_attn"] += 4.0 * cfg.num_heads * T * T * Hd
+    return out

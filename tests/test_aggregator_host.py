@@ -1,0 +1,160 @@
+"""CPU checks of the GPA aggregator harness (no GPU, no kernel calls).
+
+The schedule against aggregator.py:133-150 / :317-325, RoPE against the
+textbook rotate-half rotation of rope.py:139-209 written out per feature
+pair, the shared-set pooling against a brute-force loop over
+attention.py:113-140, the token layout of aggregator.py:249-291, and the
+FLOP accounting against the closed-form 200-frame totals.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import gpa_aggregator as A
+
+
+def test_default_schedule():
+    cfg = A.GpaConfig()
+    kinds = [cfg.block_kind(i) for i in range(cfg.depth)]
+    assert kinds[:9] == ["frame_special"] * 9
+    assert kinds[9:] == ["merged"] * 15
+    ratios = [cfg.block_merge_ratio(i) for i in range(9, 24)]
+    assert ratios == [0.98] * 4 + [0.2] * 4 + [0.98] * 7
+
+
+def test_schedule_variants():
+    van = A.vanilla_config()
+    assert all(van.block_kind(i) == "global" for i in range(24))
+    # core blocks at ratio 0 are not merged (aggregator.py:322-323)
+    cfg = A.GpaConfig(core_merge_ratio=0.0)
+    assert [cfg.block_kind(i) for i in (12, 13, 16, 17)] == ["merged", "global", "global", "merged"]
+    # merge window end
+    cfg = A.GpaConfig(merge_end=20)
+    assert cfg.block_kind(20) == "merged" and cfg.block_kind(21) == "global"
+    cfg = A.GpaConfig(merge_end=-1, early_frame_split=3, merging=5)
+    assert [cfg.block_kind(i) for i in (2, 3, 4, 5, 23)] == \
+        ["frame_special", "global", "global", "merged", "merged"]
+
+
+def _rope_textbook(x: np.ndarray, pos: np.ndarray, freq: float) -> np.ndarray:
+    """Rotate-half RoPE per axis, one feature pair at a time (fp64)."""
+    out = np.empty_like(x)
+    d = x.shape[-1]
+    half, quarter = d // 2, d // 4
+    for t in range(x.shape[-2]):
+        for a in range(2):
+            p = float(pos[t, a])
+            for j in range(quarter):
+                th = p * freq ** (-2.0 * j / half)
+                c, s = math.cos(th), math.sin(th)
+                x1 = x[..., t, a * half + j]
+                x2 = x[..., t, a * half + quarter + j]
+                out[..., t, a * half + j] = x1 * c - x2 * s
+                out[..., t, a * half + quarter + j] = x2 * c + x1 * s
+    return out
+
+
+def test_rope_matches_textbook_rotation():
+    g = torch.Generator().manual_seed(0)
+    pos = A.frame_positions(4, 5)
+    x = torch.randn(2, 3, pos.shape[0], 64, generator=g)
+    rope = A.Rope2D(100.0)
+    cos, sin = rope.tables(pos, 64)
+    got = A.Rope2D.apply(x, cos, sin).double().numpy()
+    want = _rope_textbook(x.double().numpy(), pos.numpy(), 100.0)
+    assert np.abs(got - want).max() < 2e-5
+    # specials sit at position 0: no rotation
+    assert torch.equal(A.Rope2D.apply(x, cos, sin)[..., :5, :], x[..., :5, :])
+
+
+def test_frame_positions_layout():
+    pos = A.frame_positions(37, 5)
+    assert pos.shape == (1374, 2)
+    assert (pos[:5] == 0).all()
+    assert pos[5].tolist() == [1, 1] and pos[6].tolist() == [1, 2]
+    assert pos[5 + 37].tolist() == [2, 1] and pos[-1].tolist() == [37, 37]
+
+
+def _pool_bruteforce(k5, v5, pts, grid, kp):
+    B, H, S, P, D = k5.shape
+    seeds_yx = [(y, x) for y in range(0, grid, kp) for x in range(0, grid, kp)]
+    npool = len(seeds_yx)
+    pk = np.zeros((B, H, S, npool, D))
+    pv = np.zeros((B, H, S, npool, D))
+    size = np.zeros((B, H, S, npool))
+    assign = np.zeros((B, H, S, grid * grid), dtype=np.int64)
+    k = k5.double().numpy()
+    v = v5.double().numpy()
+    for b in range(B):
+        for h in range(H):
+            for s in range(S):
+                patches = k[b, h, s, pts:]
+                seeds = np.stack([patches[y * grid + x] for y, x in seeds_yx])
+                pn = patches / np.maximum(np.linalg.norm(patches, axis=1, keepdims=True), 1e-6)
+                sn = seeds / np.maximum(np.linalg.norm(seeds, axis=1, keepdims=True), 1e-6)
+                sc = pn @ sn.T
+                top2 = np.sort(sc, axis=1)[:, -2:]
+                assert (top2[:, 1] - top2[:, 0]).min() > 1e-4, "near tie in the test data"
+                idx = sc.argmax(axis=1)
+                assign[b, h, s] = idx
+                for g in range(npool):
+                    sel = idx == g
+                    size[b, h, s, g] = sel.sum()
+                    pk[b, h, s, g] = k[b, h, s, pts:][sel].mean(axis=0)
+                    pv[b, h, s, g] = v[b, h, s, pts:][sel].mean(axis=0)
+    return pk, pv, size, assign
+
+
+def test_pool_shared_matches_bruteforce():
+    g = torch.Generator().manual_seed(1)
+    B, H, S, pts, grid, kp, D = 1, 2, 3, 5, 7, 3, 16
+    k5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
+    v5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
+    pk, pv, size, assign = A.pool_shared(k5, v5, pts, grid, kp)
+    bpk, bpv, bsize, bassign = _pool_bruteforce(k5, v5, pts, grid, kp)
+    npool = 9
+    assert np.array_equal(assign.numpy(), bassign)
+    assert np.array_equal(size.numpy(), bsize)
+    assert np.abs(pk.double().numpy().reshape(B, H, S, npool, D) - bpk).max() < 1e-5
+    assert np.abs(pv.double().numpy().reshape(B, H, S, npool, D) - bpv).max() < 1e-5
+    # every seed belongs to its own group: no empty summary
+    assert (size > 0).all() and (size.sum(-1) == grid * grid).all()
+
+
+def test_shifted_texture_images_are_translations():
+    imgs = A.shifted_texture_images(4, size=40, shift=6, seed=3)
+    assert imgs.shape == (1, 4, 3, 40, 40)
+    assert float(imgs.min()) >= 0.0 and float(imgs.max()) <= 1.0
+    g = torch.Generator().manual_seed(3)
+    tex = torch.rand(3, 46, 46, generator=g)
+    off = torch.randint(0, 6, (4, 2), generator=g).tolist()
+    for f, (y, x) in enumerate(off):
+        assert torch.equal(imgs[0, f], tex[:, y:y + 40, x:x + 40])
+
+
+def test_embed_token_layout_without_vit_blocks():
+    cfg = A.GpaConfig(vit_depth=0, depth=1, img_size=56)
+    model = A.GpaAggregator(cfg)
+    A.init_random_(model)
+    imgs = A.shifted_texture_images(3, size=56, shift=4)
+    with torch.no_grad():
+        tok = model.embed(imgs)
+    assert tok.shape == (3, 4 * 4 + 5, 1024)
+    assert torch.equal(tok[0, 0], model.camera_token[0, 0, 0])
+    assert torch.equal(tok[1, 0], model.camera_token[0, 1, 0])
+    assert torch.equal(tok[2, 1:5], model.register_token[0, 1])
+    assert torch.equal(tok[0, 1:5], model.register_token[0, 0])
+
+
+def test_aggregator_flops_closed_form():
+    cfg = A.GpaConfig()
+    f = A.aggregator_flops(cfg, 200)
+    T, H, D = 274_800, 16, 64
+    own = 4.0 * 200 * H * 1374 * 1369 * D
+    shared = 4.0 * H * T * 200 * 30 * D
+    merged = 11 * 4.0 * H * T * 66_845 * D + 4 * 4.0 * H * T * 219_840 * D
+    assert f["global_attn"] == pytest.approx(9 * (own + shared) + merged, rel=1e-12)
+    assert f["similarity"] == pytest.approx(15 * 2.0 * 207_955 * 66_845 * 128, rel=1e-12)
+    assert f["frame_attn"] == pytest.approx(48 * 4.0 * 200 * H * 1374 * 1374 * D, rel=1e-12)

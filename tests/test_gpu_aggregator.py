@@ -1,0 +1,198 @@
+"""GPU checks of the GPA aggregator harness: the merged and frame-special
+global attention of a VGGT-1B-width block against an fp32 CPU restatement.
+
+The CPU side recomputes the attention module from the block's own weights:
+qkv projection (bf16 operands, fp32 accumulation, bf16 result, as autocast
+does), qk LayerNorm, textbook RoPE, then
+  * merged block (vggt/layers/attention.py:233-268): K/V means over the
+    device merge's slot lists in fp64, bias log(size), the oracle attention;
+  * frame-special block (attention.py:148-176): per frame, one attention
+    over [own patch keys | every frame's special keys | pooled summaries]
+    with bias log(size) on the summaries -- the unsplit form the split path
+    must equal -- with the summaries averaged in fp64 over the device's
+    pool assignment;
+then the output projection.  Given identical merge / pool assignments the
+two must agree to bf16 rounding of the module's intermediates.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import gpa_aggregator as A
+import gpa_workloads as W
+from merging.merge import token_merge_bipartite2d
+from oracle.attention import attention_reference, kernel_inputs
+
+pytestmark = pytest.mark.gpu
+
+FRAMES = 3
+GRID = 37
+PTS = 5
+P = GRID * GRID + PTS
+
+
+def _rope_ref(x: torch.Tensor, pos: torch.Tensor, freq: float = 100.0) -> torch.Tensor:
+    """Rotate-half RoPE per axis (rope.py:139-209) in fp64 on the CPU."""
+    x = x.double()
+    out = x.clone()
+    j = torch.arange(16, dtype=torch.float64)
+    for a in range(2):
+        th = pos[:, a].double()[:, None] * freq ** (-2.0 * j / 32)
+        c, s = th.cos(), th.sin()
+        x1, x2 = x[..., a * 32:a * 32 + 16], x[..., a * 32 + 16:a * 32 + 32]
+        out[..., a * 32:a * 32 + 16] = x1 * c - x2 * s
+        out[..., a * 32 + 16:a * 32 + 32] = x2 * c + x1 * s
+    return out.float()
+
+
+def _block(dev, seed=0):
+    cfg = A.GpaConfig()
+    blk = A.Block(1024, 16, 4.0, 1.0, True, 1e-5, cfg).to(dev)
+    A.init_random_(blk, seed)
+    with torch.no_grad():   # non-trivial qk-norm affine parameters
+        g = torch.Generator(device=dev).manual_seed(seed + 5)
+        for ln in (blk.attn.q_norm, blk.attn.k_norm):
+            ln.weight.copy_(1 + 0.2 * torch.randn(64, generator=g, device=dev))
+            ln.bias.copy_(0.1 * torch.randn(64, generator=g, device=dev))
+    return cfg, blk.bfloat16().eval()
+
+
+def _inputs(dev):
+    x = W.shifted_basis_tokens(FRAMES, seed=4, device=dev).to(torch.bfloat16)
+    pos = A.frame_positions(GRID, PTS, dev).repeat(FRAMES, 1)
+    cos, sin = A.Rope2D(100.0).tables(pos, 64)
+    return x, pos, (cos, sin)
+
+
+def _qkv_ref(blk, xn: torch.Tensor, pos: torch.Tensor):
+    """CPU restatement of qkv -> qk-norm -> RoPE (attention.py:210-220)."""
+    at = blk.attn
+    w, b = at.qkv.weight.float().cpu(), at.qkv.bias.float().cpu()
+    x16 = xn.cpu().bfloat16().float()
+    qkv = (x16 @ w.T + b).bfloat16().float()
+    N = qkv.shape[1]
+    q, k, v = qkv.view(1, N, 3, 16, 64).permute(2, 0, 3, 1, 4).unbind(0)
+
+    def ln(t, mod):
+        return F.layer_norm(t, (64,), mod.weight.float().cpu(), mod.bias.float().cpu(), 1e-5)
+
+    q, k = ln(q, at.q_norm), ln(k, at.k_norm)
+    pc = pos.cpu()
+    return _rope_ref(q, pc), _rope_ref(k, pc), v
+
+
+def _proj_ref(blk, o: torch.Tensor) -> torch.Tensor:
+    w, b = blk.attn.proj.weight.float().cpu(), blk.attn.proj.bias.float().cpu()
+    N = o.shape[2]
+    y = o.transpose(1, 2).reshape(1, N, 1024).bfloat16().float()
+    return y @ w.T + b
+
+
+def _slot_means(t: torch.Tensor, offsets: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """fp64 mean of t [1,H,N,D] rows over CSR slot lists -> [1,H,S,D]."""
+    t64 = t.double()
+    off = offsets.cpu().numpy()
+    tok = tokens.cpu().numpy()
+    seg = np.repeat(np.arange(len(off) - 1), np.diff(off))
+    out = torch.zeros(1, t.shape[1], len(off) - 1, t.shape[3], dtype=torch.float64)
+    out.index_add_(2, torch.from_numpy(seg), t64[:, :, torch.from_numpy(tok)])
+    cnt = torch.from_numpy(np.diff(off)).double()
+    return out / cnt.view(1, 1, -1, 1)
+
+
+def _compare(got: torch.Tensor, ref: torch.Tensor, what: str):
+    err = (got.float().cpu() - ref).abs()
+    scale = ref.abs().mean().item()
+    rel_max, rel_mean = err.max().item() / scale, err.mean().item() / scale
+    print(f"[{what}] |ref| mean {scale:.3e}, max err {err.max().item():.3e} "
+          f"({rel_max:.2e} rel), mean err {err.mean().item():.3e} ({rel_mean:.2e} rel)", flush=True)
+    # bf16 intermediates (qkv, attention output, merged V) give ~1e-2 relative
+    # scatter per element; a layout, scale or bias mistake gives O(1).
+    assert rel_max < 0.06, f"{what}: max error {rel_max:.3e} of mean |ref|"
+    assert rel_mean < 0.006, f"{what}: mean error {rel_mean:.3e} of mean |ref|"
+
+
+def test_merged_block_attention_matches_reference(dev):
+    cfg, blk = _block(dev)
+    x, pos, rope = _inputs(dev)
+    N = x.shape[1]
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        xn = blk.norm1(x)
+        got = blk.attn(xn, rope, 9)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(A.MERGE_GENERATOR_SEED)
+        m = token_merge_bipartite2d(xn, GRID, GRID, 2, 2, int(N * 0.98), False, gen,
+                                    metric_dim=128, num_special=PTS)
+    assert xn.dtype == torch.float32
+    q, k, v = _qkv_ref(blk, xn, pos)
+    off, tok = m.index.slot_offsets, m.index.slot_tokens
+    km = _slot_means(k, off, tok).float()
+    vm = _slot_means(v, off, tok)
+    size = m.size.cpu()
+    assert km.shape[2] == size.shape[1] == m.index.num_dst   # all sources merged at 0.98
+    bias = size.log().view(1, 1, 1, -1)
+    o, _ = attention_reference(*kernel_inputs(q, km, vm.float(), bias.expand(1, 16, 1, -1)),
+                               blk.attn.scale)
+    _compare(got, _proj_ref(blk, o), "merged block")
+
+
+def test_frame_special_block_attention_matches_reference(dev):
+    cfg, blk = _block(dev, seed=1)
+    blk.attn.frame_special = True
+    x, pos, rope = _inputs(dev)
+    N = x.shape[1]
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        xn = blk.norm1(x)
+        got = blk.attn(xn, rope, None)
+        # the device's pool assignment, from the module's own K/V
+        qkv = blk.attn.qkv(xn).view(1, N, 3, 16, 64).permute(2, 0, 3, 1, 4)
+        kd = A.Rope2D.apply(blk.attn.k_norm(qkv[1]), *rope).to(torch.bfloat16)
+        vd = qkv[2]
+        _, _, size_d, assign_d = A.pool_shared(kd.view(1, 16, FRAMES, P, 64),
+                                               vd.reshape(1, 16, FRAMES, P, 64), PTS, GRID, 8)
+    q, k, v = _qkv_ref(blk, xn, pos)
+    q16, k16, v16 = q.bfloat16().float(), k.bfloat16().float(), v
+    k5, v5 = k16.view(1, 16, FRAMES, P, 64), v16.view(1, 16, FRAMES, P, 64)
+    assign = assign_d.cpu()
+    npool = 25
+    onehot = F.one_hot(assign, npool).double()                     # [1,16,S,1369,25]
+    cnt = onehot.sum(3)                                            # [1,16,S,25]
+    assert torch.equal(cnt.float(), size_d.cpu())
+    pk = torch.einsum("bhspg,bhspd->bhsgd", onehot, k5[:, :, :, PTS:].double()) / cnt[..., None]
+    pv = torch.einsum("bhspg,bhspd->bhsgd", onehot, v5[:, :, :, PTS:].double()) / cnt[..., None]
+    sp_k = k5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
+    sp_v = v5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
+    out = torch.empty(1, 16, N, 64)
+    for s in range(FRAMES):
+        kk = torch.cat([k5[:, :, s, PTS:], sp_k, pk.reshape(1, 16, -1, 64).float()], dim=2)
+        vv = torch.cat([v5[:, :, s, PTS:], sp_v, pv.reshape(1, 16, -1, 64).float()], dim=2)
+        bias = torch.zeros(1, 16, 1, kk.shape[2])
+        bias[..., GRID * GRID + FRAMES * PTS:] = cnt.reshape(1, 16, -1).log().float()[:, :, None]
+        o, _ = attention_reference(*kernel_inputs(q16[:, :, s * P:(s + 1) * P], kk, vv, bias),
+                                   blk.attn.scale)
+        out[:, :, s * P:(s + 1) * P] = o
+    _compare(got, _proj_ref(blk, out), "frame-special block")
+
+
+def test_small_aggregator_runs_every_global_path(dev):
+    cfg = A.GpaConfig(depth=3, vit_depth=1, early_frame_split=1, merging=1,
+                      core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2))
+    assert [cfg.block_kind(i) for i in range(3)] == ["frame_special", "merged", "merged"]
+    model = A.build_aggregator(cfg, device=dev, seed=2)
+    imgs = A.shifted_texture_images(FRAMES, device=dev).to(torch.bfloat16)
+    tracer = A.StageTimer()
+    model.set_tracer(tracer)
+    tracer.start()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outs = model(imgs)
+    stages = tracer.totals()
+    assert {"frame_special_attn", "pool", "merge", "merged_attn", "frame_attn"} <= set(stages)
+    assert len(outs) == 3
+    for o in outs:
+        assert o.shape == (1, FRAMES, P, 2048) and o.dtype == torch.bfloat16
+        assert torch.isfinite(o).all()
+    flops = A.aggregator_flops(cfg, FRAMES)
+    assert flops["similarity"] > 0 and flops["global_attn"] > 0
