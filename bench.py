@@ -85,13 +85,13 @@ def e2e_latency(dev) -> dict:
     imgs = A.shifted_texture_images(frames, device=dev).to(bf16)
     with torch.no_grad(), torch.autocast("cuda", dtype=bf16):
         tokens = model.embed(imgs).reshape(1, frames * cfg.tokens_per_frame, cfg.embed_dim)
-    _, _, cos, sin = model.rope_tables(frames, dev)
+    rope = model.rope_table(dev)
     blk = model.global_blocks[9]
-    ms, peak = A.timed(run(lambda: blk(tokens, (cos, sin), 9)))
+    ms, peak = A.timed(run(lambda: blk(tokens, rope, 9)))
     res["gpa_block_100f"] = {
         "ms": round(ms, 2), "peak_gib": round(peak, 2),
         "workload": "merged global block 9 (ratio 0.98): 137,400 tokens -> 33,945 merged keys"}
-    del tokens, imgs, cos, sin
+    del tokens, imgs
     log(f"[bench] GPA block 100 frames: {ms:.1f} ms")
 
     frames = 200

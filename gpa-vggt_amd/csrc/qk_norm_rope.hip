@@ -1,0 +1,194 @@
+// Fused qk LayerNorm + 2D rotary embedding + cast: the attention operands of
+// a VGGT block straight from its QKV projection.
+//
+// For every token n and head h of the projection rows qkv[b, n, :]
+// (q at column h*64, k at column k_offset + h*64), with x the 64 bf16
+// features:
+//
+//   y = (x - mean(x)) / sqrt(var(x) + eps) * w + beta          (fp32)
+//   out[j]      = y[j] cos(p a_j) - y[j+16] sin(p a_j)   j in [0,16) of each 32-half
+//   out[j + 16] = y[j+16] cos(p a_j) + y[j] sin(p a_j)
+//
+// where the first 32 features rotate with the token's row coordinate and the
+// last 32 with its column coordinate (p from pos[n mod period]), and the
+// (cos, sin) of p * a_j come from a host-built table.  Output is written
+// head-major [B, H, N, 64], the layout of the attention kernel and of the
+// K/V merge, once, in bf16 or fp32.
+//
+// This replaces the torch op sequence of vggt/layers/attention.py:210-220
+// (q_norm / k_norm LayerNorm, then vggt/layers/rope.py:167-209 on q and k,
+// then the bf16 cast of merging/fused_attention.py:139-144): about ten
+// passes over fp32 [B, H, N, 64] tensors become one read of the bf16
+// projection and one write.
+//
+// Work split: eight lanes own one (token, head, q|k) row, 16 bytes each;
+// the LayerNorm moments and the rotation partner (feature j <-> j+16 is lane
+// c <-> c^2 within the eight) are cross-lane exchanges.  A workgroup handles
+// 32 consecutive tokens of one (q|k, head), so its writes are one contiguous
+// 4 KB (bf16) run.  HBM-bound.
+#include "gpa_common.h"
+
+namespace gpa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kLanesPerRow = 8;
+constexpr int kRowsPerBlock = kThreads / kLanesPerRow;
+constexpr int kHeadDim = 64;
+
+struct QkArgs {
+  const uint16_t* qkv;
+  int64_t sb, sn, k_offset;
+  const float* w;      // [2][64]: q then k
+  const float* beta;   // [2][64]
+  float eps;
+  const int32_t* pos;  // [period][2] or null (no rotation)
+  int64_t period;
+  const float* cs;     // [npos][16][2] (cos, sin)
+  int32_t npos;
+  void* q_out;
+  void* k_out;
+  int q_f32, k_f32;
+  int64_t B, N, H;
+  int64_t rows;        // B * N
+};
+
+__device__ __forceinline__ float group_sum8(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  return v;
+}
+
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
+  const int which = blockIdx.y & 1;            // 0: q, 1: k
+  const int64_t h = blockIdx.y >> 1;
+  const int c = threadIdx.x % kLanesPerRow;    // features 8c .. 8c+7
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
+  const bool valid = row < a.rows;
+  const int64_t rc = valid ? row : a.rows - 1;  // every lane joins the exchanges
+  const int64_t b = rc / a.N, n = rc % a.N;
+
+  const bf16x8 xv = *reinterpret_cast<const bf16x8*>(
+      a.qkv + b * a.sb + n * a.sn + which * a.k_offset + h * kHeadDim + c * 8);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)xv[i];
+
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i];
+  const float mean = group_sum8(s) * (1.0f / kHeadDim);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x[i] -= mean;
+    ss += x[i] * x[i];
+  }
+  const float rstd = rsqrtf(group_sum8(ss) * (1.0f / kHeadDim) + a.eps);
+  const float* w = a.w + which * kHeadDim + c * 8;
+  const float* be = a.beta + which * kHeadDim + c * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = x[i] * rstd * w[i] + be[i];
+
+  if (a.pos != nullptr) {
+    int p = a.pos[(n % a.period) * 2 + (c >= 4 ? 1 : 0)];
+    p = p < 0 ? 0 : (p >= a.npos ? a.npos - 1 : p);
+    const float sgn = (c & 2) ? 1.0f : -1.0f;   // second quarter of a half: +, first: -
+    const float2* cs = reinterpret_cast<const float2*>(a.cs) + (int64_t)p * 16 + (c & 1) * 8;
+    float partner[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) partner[i] = __shfl_xor(x[i], 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float2 t = cs[i];
+      x[i] = __builtin_fmaf(x[i], t.x, sgn * partner[i] * t.y);
+    }
+  }
+  if (!valid) return;
+
+  const int64_t o = ((b * a.H + h) * a.N + n) * kHeadDim + c * 8;
+  void* out = which ? a.k_out : a.q_out;
+  if (which ? a.k_f32 : a.q_f32) {
+    f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(out) + o);
+    dst[0] = f32x4{x[0], x[1], x[2], x[3]};
+    dst[1] = f32x4{x[4], x[5], x[6], x[7]};
+  } else {
+    bf16x8 yv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) yv[i] = (__bf16)x[i];
+    *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + o) = yv;
+  }
+}
+
+}  // namespace
+}  // namespace gpa
+
+using namespace gpa;
+
+extern "C" int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H,
+                                     int64_t D, int64_t qkv_sb, int64_t qkv_sn,
+                                     int64_t k_offset, const float* ln_weight,
+                                     const float* ln_bias, float eps, const int32_t* pos,
+                                     int64_t period, const float* rope_cs, int64_t npos,
+                                     void* q_out, int q_dtype, void* k_out, int k_dtype,
+                                     void* stream) {
+  gpa_clear_error();
+  if (B < 0 || N < 0 || H < 0) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: negative size");
+    return GPA_E_INVALID;
+  }
+  if (D != kHeadDim) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: head dim %lld is not implemented (64 only)",
+                  (long long)D);
+    return GPA_E_UNSUPPORTED;
+  }
+  if (B == 0 || N == 0 || H == 0) return GPA_OK;
+  if (!qkv || !ln_weight || !ln_bias || !q_out || !k_out) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: null pointer");
+    return GPA_E_INVALID;
+  }
+  if (pos != nullptr && (period <= 0 || rope_cs == nullptr || npos <= 0 || npos > (1 << 20))) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: rotation needs period > 0, a table and 0 < npos <= 2^20");
+    return GPA_E_INVALID;
+  }
+  for (int dt : {q_dtype, k_dtype}) {
+    if (dt != GPA_DTYPE_F32 && dt != GPA_DTYPE_BF16) {
+      gpa_set_error("gpa_qk_norm_rope_bf16: output dtype %d is not fp32 or bf16", dt);
+      return GPA_E_UNSUPPORTED;
+    }
+  }
+  const bool aligned = (uintptr_t)qkv % 16 == 0 && (uintptr_t)q_out % 16 == 0 &&
+                       (uintptr_t)k_out % 16 == 0 && (B == 1 || qkv_sb % 8 == 0) &&
+                       (N == 1 || qkv_sn % 8 == 0) && k_offset % 8 == 0 && k_offset >= H * D;
+  if (!aligned) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: rows must be 16-byte aligned and k must follow q "
+                  "(k_offset >= H*64, multiple of 8)");
+    return GPA_E_INVALID;
+  }
+  if (2 * H > 65535) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: too many heads");
+    return GPA_E_UNSUPPORTED;
+  }
+  QkArgs a{};
+  a.qkv = (const uint16_t*)qkv;
+  a.sb = qkv_sb; a.sn = qkv_sn; a.k_offset = k_offset;
+  a.w = ln_weight; a.beta = ln_bias; a.eps = eps;
+  a.pos = pos; a.period = period; a.cs = rope_cs; a.npos = (int32_t)npos;
+  a.q_out = q_out; a.k_out = k_out;
+  a.q_f32 = q_dtype == GPA_DTYPE_F32; a.k_f32 = k_dtype == GPA_DTYPE_F32;
+  a.B = B; a.N = N; a.H = H; a.rows = B * N;
+  const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks > 0x7fffffff) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: problem exceeds the grid limit");
+    return GPA_E_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks, (unsigned)(2 * H)),
+                     dim3(kThreads), 0, (hipStream_t)stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    gpa_set_error("gpa_qk_norm_rope_bf16: launch failed: %s", hipGetErrorString(e));
+    return GPA_E_LAUNCH;
+  }
+  return GPA_OK;
+}

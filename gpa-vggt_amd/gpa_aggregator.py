@@ -32,15 +32,19 @@ N(0, 0.02^2), biases 0, LayerNorm weight 1 / bias 0, LayerScale gammas at the
 reference's init values.  Run under `torch.autocast("cuda", bf16)` on a
 bf16 model, as eval/bench_e2e.py:76-92 does.
 
-Known departure: RoPE angles are computed in fp32 (cos/sin of p * f);
-the reference builds them through an einsum that autocast may run in bf16.
+The qk LayerNorm, RoPE and bf16 cast of every aggregator block run as one
+fused kernel (`gpa::qk_norm_rope`) instead of the reference's separate torch
+ops; K stays fp32 for the merge in merged blocks, as in the reference.
+
+Known departure: RoPE angles are evaluated in fp64 and rounded once (a
+table of cos/sin of p * f); the reference builds them through an einsum
+that autocast may run in bf16.
 """
 from __future__ import annotations
 
-import math
 import time
-from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Tuple
+from dataclasses import dataclass
+from typing import Dict, List, NamedTuple, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -121,31 +125,35 @@ def vanilla_config(**kw) -> GpaConfig:
 # building blocks
 # ---------------------------------------------------------------------------
 
+class RopeTable(NamedTuple):
+    """Positions [P, 2] int32 of one frame's tokens (token n uses row
+    n mod P) and the (cos, sin) table [npos, head_dim/4, 2] fp32."""
+    pos: torch.Tensor
+    cs: torch.Tensor
+
+
 class Rope2D:
     """2D rotary embedding: the first half of each head's features rotates
     with the row coordinate, the second half with the column coordinate, each
     half as [x1, x2] -> [x1 cos - x2 sin, x2 cos + x1 sin] with frequencies
-    freq^(-2i/half) (rope.py:92-209)."""
+    freq^(-2i/half) (rope.py:92-209).  The rotation itself runs fused with
+    the qk LayerNorm in the `gpa::qk_norm_rope` kernel."""
 
     def __init__(self, freq: float):
         self.freq = freq
 
-    def tables(self, pos: torch.Tensor, head_dim: int) -> Tuple[torch.Tensor, torch.Tensor]:
-        """pos [T, 2] int -> (cos, sin) [T, head_dim] fp32."""
+    def cs_table(self, npos: int, head_dim: int, device="cpu") -> torch.Tensor:
+        """[npos, head_dim/4, 2] fp32: (cos, sin) of p * freq^(-2j/(head_dim/2)),
+        evaluated in fp64 and rounded once."""
         half = head_dim // 2
-        inv = self.freq ** (-torch.arange(0, half, 2, dtype=torch.float64,
-                                          device=pos.device) / half)
-        ang = pos.to(torch.float64)[..., None] * inv               # [T, 2, half/2]
-        ang = torch.cat((ang, ang), dim=-1).reshape(pos.shape[0], head_dim)
-        return ang.cos().float(), ang.sin().float()
+        inv = self.freq ** (-torch.arange(0, half, 2, dtype=torch.float64) / half)
+        ang = torch.arange(npos, dtype=torch.float64)[:, None] * inv
+        return torch.stack((ang.cos(), ang.sin()), dim=-1).float().to(device)
 
-    @staticmethod
-    def apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        """x [..., T, D] (any float dtype), cos/sin [T, D] -> rotated x."""
-        d = x.shape[-1]
-        xr = x.unflatten(-1, (2, 2, d // 4))
-        rot = torch.stack((-xr[..., 1, :], xr[..., 0, :]), dim=-2).flatten(-3)
-        return x * cos.to(x.dtype) + rot * sin.to(x.dtype)
+    def table(self, pos: torch.Tensor, head_dim: int) -> RopeTable:
+        npos = int(pos.max()) + 1
+        return RopeTable(pos.to(torch.int32).contiguous(),
+                         self.cs_table(npos, head_dim, pos.device))
 
 
 class LayerScale(nn.Module):
@@ -194,15 +202,39 @@ class GpaAttention(nn.Module):
         if self.tracer is not None:
             self.tracer.mark(name)
 
-    def forward(self, x: torch.Tensor, rope_cs=None, global_merging: Optional[int] = None):
+    def qk(self, x: torch.Tensor, rope: Optional[RopeTable], k_f32: bool = False):
+        """q, k, v [B, H, N, D] from the block input (attention.py:210-220).
+
+        With qk LayerNorm the normalisation, the rotation and the cast run
+        as one `gpa::qk_norm_rope` kernel over the bf16 projection (q bf16;
+        k fp32 when `k_f32`, for the K merge, else bf16); v stays a view of
+        the projection.  Without it (the patch embedder's blocks) q, k, v
+        are all views of the projection.
+        """
         B, N, C = x.shape
         H, D = self.heads, self.head_dim
-        qkv = self.qkv(x).view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
-        q, k, v = qkv.unbind(0)
-        q, k = self.q_norm(q), self.k_norm(k)
-        if rope_cs is not None:
-            cos, sin = rope_cs
-            q, k = Rope2D.apply(q, cos, sin), Rope2D.apply(k, cos, sin)
+        qkv = self.qkv(x)
+        v = qkv.view(B, N, 3, H, D)[:, :, 2].transpose(1, 2)
+        if isinstance(self.q_norm, nn.LayerNorm):
+            if qkv.dtype != torch.bfloat16:
+                raise ValueError("the fused qk-norm/RoPE kernel takes a bf16 projection "
+                                 "(run the bf16 model under autocast)")
+            ln_w = torch.stack((self.q_norm.weight, self.k_norm.weight))
+            ln_b = torch.stack((self.q_norm.bias, self.k_norm.bias))
+            q, k = torch.ops.gpa.qk_norm_rope(
+                qkv, ln_w, ln_b, self.q_norm.eps, None if rope is None else rope.pos,
+                None if rope is None else rope.cs, H, False, k_f32)
+            return q, k, v
+        if rope is not None:
+            raise ValueError("RoPE without qk LayerNorm is not implemented")
+        t = qkv.view(B, N, 3, H, D)
+        return t[:, :, 0].transpose(1, 2), t[:, :, 1].transpose(1, 2), v
+
+    def forward(self, x: torch.Tensor, rope: Optional[RopeTable] = None,
+                global_merging: Optional[int] = None):
+        B, N, C = x.shape
+        H, D = self.heads, self.head_dim
+        q, k, v = self.qk(x, rope, k_f32=global_merging is not None and not self.frame_special)
         self._mark("qkv")
 
         if self.frame_special:
@@ -311,8 +343,8 @@ class Block(nn.Module):
         self.mlp = Mlp(dim, int(dim * mlp_ratio))
         self.ls2 = LayerScale(dim, ls_init)
 
-    def forward(self, x, rope_cs=None, global_merging=None):
-        x = x + self.ls1(self.attn(self.norm1(x), rope_cs, global_merging))
+    def forward(self, x, rope: Optional[RopeTable] = None, global_merging=None):
+        x = x + self.ls1(self.attn(self.norm1(x), rope, global_merging))
         return x + self.ls2(self.mlp(self.norm2(x)))
 
 
@@ -412,22 +444,21 @@ class GpaAggregator(nn.Module):
         reg = _first_vs_rest(self.register_token, B, S)
         return torch.cat((cam, reg, patches), dim=1).to(dt)
 
-    def rope_tables(self, frames: int, device):
-        cos, sin = self.rope.tables(self.positions(device), self.cfg.embed_dim // self.cfg.num_heads)
-        return cos, sin, cos.repeat(frames, 1), sin.repeat(frames, 1)
+    def rope_table(self, device) -> RopeTable:
+        return self.rope.table(self.positions(device), self.cfg.embed_dim // self.cfg.num_heads)
 
     def forward(self, images: torch.Tensor) -> List[torch.Tensor]:
         B, S = images.shape[:2]
         tokens = self.embed(images)
         self._mark("patch_embed")
         P, C = tokens.shape[1], tokens.shape[2]
-        cos_f, sin_f, cos_g, sin_g = self.rope_tables(S, images.device)
+        rope = self.rope_table(images.device)
         outputs = []
         for i in range(self.cfg.depth):
-            tokens = self.frame_blocks[i](tokens.view(B * S, P, C), (cos_f, sin_f))
+            tokens = self.frame_blocks[i](tokens.view(B * S, P, C), rope)
             self._mark("frame_block")
             frame_out = tokens.view(B, S, P, C)
-            tokens = self.global_blocks[i](tokens.view(B, S * P, C), (cos_g, sin_g),
+            tokens = self.global_blocks[i](tokens.view(B, S * P, C), rope,
                                            self.cfg.global_merging(i))
             self._mark(f"global_block_{self.cfg.block_kind(i)}")
             if i in self.cfg.dpt_blocks:

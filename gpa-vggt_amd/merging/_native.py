@@ -13,6 +13,9 @@ two custom ops:
                      bool mean) -> (Tensor out, Tensor size, Tensor log_size)
     gpa::lse_combine(Tensor out_a, Tensor lse_a, Tensor out_b, Tensor lse_b,
                      int frames) -> Tensor y
+    gpa::qk_norm_rope(Tensor qkv, Tensor ln_w, Tensor ln_b, float eps,
+                      Tensor? pos, Tensor? rope_cs, int heads, bool q_f32,
+                      bool k_f32) -> (Tensor q, Tensor k)
 
 All launch on torch's current stream of the input's device.  There is no
 fallback: a missing library or a non-GPU tensor raises.
@@ -27,7 +30,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -90,6 +93,15 @@ def _bind(lib: ctypes.CDLL) -> None:
     ]
     lib.gpa_lse_combine_bf16.restype = ctypes.c_int
     lib.gpa_lse_combine_bf16.argtypes = [_vp] * 5 + [_i64] * 5 + [_i64] * 16 + [_i64] * 3 + [_vp]
+    lib.gpa_qk_norm_rope_bf16.restype = ctypes.c_int
+    lib.gpa_qk_norm_rope_bf16.argtypes = [
+        _vp, _i64, _i64, _i64, _i64,   # qkv, B, N, H, D
+        _i64, _i64, _i64,              # qkv_sb, qkv_sn, k_offset
+        _vp, _vp, ctypes.c_float,      # ln_weight, ln_bias, eps
+        _vp, _i64, _vp, _i64,          # pos, period, rope_cs, npos
+        _vp, ctypes.c_int, _vp, ctypes.c_int,  # q_out, q_dtype, k_out, k_dtype
+        _vp,                           # stream
+    ]
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -125,7 +137,7 @@ def lib() -> ctypes.CDLL:
 def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
-            "gpa_merge_heads", "gpa_lse_combine_bf16")
+            "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -391,3 +403,63 @@ def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
 def _lse_combine_fake(out_a, lse_a, out_b, lse_b, frames):
     B, H, N, D = out_b.shape
     return out_b.new_empty(B, N, H * D, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("gpa::qk_norm_rope", mutates_args=())
+def qk_norm_rope(qkv: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, eps: float,
+                 pos: Optional[torch.Tensor], rope_cs: Optional[torch.Tensor], heads: int,
+                 q_f32: bool, k_f32: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """qk LayerNorm + 2D RoPE of the QKV projection qkv [B, N, >= 3*heads*64]
+    (bf16): returns q, k [B, heads, N, 64] (fp32 or bf16 each).
+
+    ln_w / ln_b [2, 64]: the q and k LayerNorm affine parameters; pos
+    [period, 2] int32 (token n uses row n mod period) and rope_cs
+    [npos, 16, 2] fp32 (cos, sin) tables, or both None for no rotation.
+    """
+    dev = _require_gpu(qkv, ln_w, ln_b)
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 3:
+        raise ValueError(f"gpa::qk_norm_rope: qkv must be bf16 [B, N, 3C], got {qkv.dtype} "
+                         f"{tuple(qkv.shape)}")
+    H = int(heads)
+    if H <= 0 or qkv.shape[2] < 3 * H * 64:
+        raise ValueError(f"gpa::qk_norm_rope: rows of {qkv.shape[2]} cannot hold q, k, v of "
+                         f"{H} heads x 64")
+    w = ln_w.to(device=dev, dtype=torch.float32).contiguous()
+    bb = ln_b.to(device=dev, dtype=torch.float32).contiguous()
+    if w.numel() != 128 or bb.numel() != 128:
+        raise ValueError("gpa::qk_norm_rope: ln_w and ln_b hold the q and k weights, 2 x 64")
+    if (pos is None) != (rope_cs is None):
+        raise ValueError("gpa::qk_norm_rope: pos and rope_cs go together")
+    period, npos = 0, 0
+    if pos is not None:
+        _require_gpu(pos, rope_cs)
+        if pos.dtype != torch.int32 or pos.dim() != 2 or pos.shape[1] != 2:
+            raise ValueError("gpa::qk_norm_rope: pos must be int32 [period, 2]")
+        if rope_cs.dtype != torch.float32 or rope_cs.shape[1:] != (16, 2):
+            raise ValueError("gpa::qk_norm_rope: rope_cs must be fp32 [npos, 16, 2]")
+        pos, rope_cs = pos.contiguous(), rope_cs.contiguous()
+        period, npos = pos.shape[0], rope_cs.shape[0]
+    if not _rows_ok(qkv, 8):
+        qkv = qkv.contiguous()
+    B, N, _ = qkv.shape
+    q = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if q_f32 else torch.bfloat16)
+    k = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if k_f32 else torch.bfloat16)
+    if q.numel() == 0:
+        return q, k
+    with torch.cuda.device(dev):
+        rc = lib().gpa_qk_norm_rope_bf16(
+            qkv.data_ptr(), B, N, H, 64, _st(qkv, 0), _rs(qkv, 1), H * 64,
+            w.data_ptr(), bb.data_ptr(), float(eps),
+            pos.data_ptr() if pos is not None else None, period,
+            rope_cs.data_ptr() if rope_cs is not None else None, npos,
+            q.data_ptr(), GPA_DTYPE_F32 if q_f32 else GPA_DTYPE_BF16,
+            k.data_ptr(), GPA_DTYPE_F32 if k_f32 else GPA_DTYPE_BF16, _stream(dev))
+    _check(rc, "gpa::qk_norm_rope")
+    return q, k
+
+
+@qk_norm_rope.register_fake
+def _qk_norm_rope_fake(qkv, ln_w, ln_b, eps, pos, rope_cs, heads, q_f32, k_f32):
+    B, N, _ = qkv.shape
+    return (qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if q_f32 else torch.bfloat16),
+            qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if k_f32 else torch.bfloat16))

@@ -15,6 +15,9 @@
  *                           merging/merge.py:234-250).
  *   gpa_lse_combine_bf16  — merge of two partial attentions by their log2
  *                           LSE (replaces vggt/layers/attention.py:166-176).
+ *   gpa_qk_norm_rope_bf16 — qk LayerNorm + 2D RoPE + cast of a block's
+ *                           attention operands (replaces the torch op
+ *                           sequence of vggt/layers/attention.py:210-220).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -38,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 3
+#define GPA_ABI_VERSION 4
 
 enum {
   GPA_OK = 0,
@@ -162,6 +165,32 @@ int gpa_lse_combine_bf16(const void* oa, const float* la, const void* ob, const 
                          int64_t ob_b, int64_t ob_h, int64_t ob_s, int64_t ob_p,
                          int64_t lb_b, int64_t lb_h, int64_t lb_s, int64_t lb_p,
                          int64_t y_b, int64_t y_n, int64_t y_h, void* stream);
+
+/*
+ * qk LayerNorm + 2D rotary embedding + cast, from the QKV projection rows.
+ * For each token n < N of batch b and head h < H (D must be 64):
+ *   x = qkv[b*qkv_sb + n*qkv_sn + h*64 .. +64]              (q; k at + k_offset)
+ *   y = (x - mean) / sqrt(var + eps) * w + beta              (fp32; biased variance)
+ *   within each 32-feature half (first: row coordinate, second: column
+ *   coordinate of pos[(n mod period)*2 + half]), for j < 16:
+ *     out[j] = y[j] c - y[j+16] s,  out[j+16] = y[j+16] c + y[j] s
+ *   with (c, s) = rope_cs[(p*16 + j)*2 + {0,1}] (positions clamped to
+ *   [0, npos)); pos == NULL skips the rotation.
+ * ln_weight / ln_bias hold 128 floats each: q's 64, then k's 64.  q_out and
+ * k_out are contiguous [B, H, N, 64] of q_dtype / k_dtype (GPA_DTYPE_F32 or
+ * GPA_DTYPE_BF16).  qkv rows: bf16, unit feature stride, 16-byte aligned,
+ * each holding at least k_offset + H*64 elements (k_offset >= H*64).
+ * Replaces q_norm / k_norm and the RoPE of vggt/layers/attention.py:216-220
+ * (vggt/layers/rope.py:167-209) and the fp32 -> bf16 cast of
+ * merging/fused_attention.py:139-144; the reference module interface has no
+ * such entry point (it runs these as separate torch ops).
+ */
+int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H, int64_t D,
+                          int64_t qkv_sb, int64_t qkv_sn, int64_t k_offset,
+                          const float* ln_weight, const float* ln_bias, float eps,
+                          const int32_t* pos, int64_t period,
+                          const float* rope_cs, int64_t npos,
+                          void* q_out, int q_dtype, void* k_out, int k_dtype, void* stream);
 
 #ifdef __cplusplus
 }

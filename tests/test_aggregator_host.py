@@ -1,8 +1,8 @@
 """CPU checks of the GPA aggregator harness (no GPU, no kernel calls).
 
-The schedule against aggregator.py:133-150 / :317-325, RoPE against the
-textbook rotate-half rotation of rope.py:139-209 written out per feature
-pair, the shared-set pooling against a brute-force loop over
+The schedule against aggregator.py:133-150 / :317-325, the RoPE angle table
+against the frequencies of rope.py:92-123 (the rotation itself runs in the
+fused qk kernel and is pinned on the GPU), the shared-set pooling against a brute-force loop over
 attention.py:113-140, the token layout of aggregator.py:249-291, and the
 FLOP accounting against the closed-form 200-frame totals.
 """
@@ -38,35 +38,17 @@ def test_schedule_variants():
         ["frame_special", "global", "global", "merged", "merged"]
 
 
-def _rope_textbook(x: np.ndarray, pos: np.ndarray, freq: float) -> np.ndarray:
-    """Rotate-half RoPE per axis, one feature pair at a time (fp64)."""
-    out = np.empty_like(x)
-    d = x.shape[-1]
-    half, quarter = d // 2, d // 4
-    for t in range(x.shape[-2]):
-        for a in range(2):
-            p = float(pos[t, a])
-            for j in range(quarter):
-                th = p * freq ** (-2.0 * j / half)
-                c, s = math.cos(th), math.sin(th)
-                x1 = x[..., t, a * half + j]
-                x2 = x[..., t, a * half + quarter + j]
-                out[..., t, a * half + j] = x1 * c - x2 * s
-                out[..., t, a * half + quarter + j] = x2 * c + x1 * s
-    return out
-
-
-def test_rope_matches_textbook_rotation():
-    g = torch.Generator().manual_seed(0)
-    pos = A.frame_positions(4, 5)
-    x = torch.randn(2, 3, pos.shape[0], 64, generator=g)
+def test_rope_table_matches_textbook_angles():
     rope = A.Rope2D(100.0)
-    cos, sin = rope.tables(pos, 64)
-    got = A.Rope2D.apply(x, cos, sin).double().numpy()
-    want = _rope_textbook(x.double().numpy(), pos.numpy(), 100.0)
-    assert np.abs(got - want).max() < 2e-5
-    # specials sit at position 0: no rotation
-    assert torch.equal(A.Rope2D.apply(x, cos, sin)[..., :5, :], x[..., :5, :])
+    cs = rope.cs_table(40, 64)
+    assert cs.shape == (40, 16, 2) and cs.dtype == torch.float32
+    for p in (0, 1, 7, 39):
+        for j in range(16):
+            th = p * 100.0 ** (-2.0 * j / 32)      # rope.py:109-114: base^(-2j/dim), dim 32
+            assert abs(float(cs[p, j, 0]) - math.cos(th)) < 1e-7
+            assert abs(float(cs[p, j, 1]) - math.sin(th)) < 1e-7
+    t = rope.table(A.frame_positions(37, 5), 64)
+    assert t.pos.dtype == torch.int32 and t.cs.shape == (38, 16, 2)
 
 
 def test_frame_positions_layout():

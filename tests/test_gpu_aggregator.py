@@ -14,8 +14,6 @@ does), qk LayerNorm, textbook RoPE, then
 then the output projection.  Given identical merge / pool assignments the
 two must agree to bf16 rounding of the module's intermediates.
 """
-import math
-
 import numpy as np
 import pytest
 import torch
@@ -62,9 +60,8 @@ def _block(dev, seed=0):
 
 def _inputs(dev):
     x = W.shifted_basis_tokens(FRAMES, seed=4, device=dev).to(torch.bfloat16)
-    pos = A.frame_positions(GRID, PTS, dev).repeat(FRAMES, 1)
-    cos, sin = A.Rope2D(100.0).tables(pos, 64)
-    return x, pos, (cos, sin)
+    pos1 = A.frame_positions(GRID, PTS, dev)
+    return x, pos1.repeat(FRAMES, 1), A.Rope2D(100.0).table(pos1, 64)
 
 
 def _qkv_ref(blk, xn: torch.Tensor, pos: torch.Tensor):
@@ -148,9 +145,7 @@ def test_frame_special_block_attention_matches_reference(dev):
         xn = blk.norm1(x)
         got = blk.attn(xn, rope, None)
         # the device's pool assignment, from the module's own K/V
-        qkv = blk.attn.qkv(xn).view(1, N, 3, 16, 64).permute(2, 0, 3, 1, 4)
-        kd = A.Rope2D.apply(blk.attn.k_norm(qkv[1]), *rope).to(torch.bfloat16)
-        vd = qkv[2]
+        _, kd, vd = blk.attn.qk(xn, rope)
         _, _, size_d, assign_d = A.pool_shared(kd.view(1, 16, FRAMES, P, 64),
                                                vd.reshape(1, 16, FRAMES, P, 64), PTS, GRID, 8)
     q, k, v = _qkv_ref(blk, xn, pos)
@@ -196,3 +191,34 @@ def test_small_aggregator_runs_every_global_path(dev):
         assert torch.isfinite(o).all()
     flops = A.aggregator_flops(cfg, FRAMES)
     assert flops["similarity"] > 0 and flops["global_attn"] > 0
+
+
+@pytest.mark.parametrize("frames,k_f32", [(3, True), (2, False)])
+def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32):
+    """gpa::qk_norm_rope against LayerNorm + rotate-half RoPE in fp64."""
+    g = torch.Generator(device=dev).manual_seed(frames)
+    N = frames * P
+    qkv = (torch.randn(1, N, 3 * 1024, generator=g, device=dev) * 1.5 + 0.3).bfloat16()
+    ln_w = 1 + 0.3 * torch.randn(2, 64, generator=g, device=dev)
+    ln_b = 0.2 * torch.randn(2, 64, generator=g, device=dev)
+    pos1 = A.frame_positions(GRID, PTS, dev)
+    rope = A.Rope2D(100.0).table(pos1, 64)
+    q, k = torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, rope.pos, rope.cs, 16, False, k_f32)
+    assert q.dtype == torch.bfloat16 and q.shape == (1, 16, N, 64)
+    assert k.dtype == (torch.float32 if k_f32 else torch.bfloat16)
+    x = qkv.cpu().double().view(1, N, 3, 16, 64).permute(2, 0, 3, 1, 4)
+    pos = pos1.cpu().repeat(frames, 1)
+    for got, t, i in ((q, x[0], 0), (k, x[1], 1)):
+        mu = t.mean(-1, keepdim=True)
+        var = ((t - mu) ** 2).mean(-1, keepdim=True)
+        y = (t - mu) / torch.sqrt(var + 1e-5) * ln_w[i].cpu().double() + ln_b[i].cpu().double()
+        want = _rope_ref(y, pos).double()
+        err = (got.cpu().double() - want).abs()
+        bound = (2.0 ** -8 if got.dtype == torch.bfloat16 else 1e-5) * want.abs() + 1e-5
+        assert (err <= bound).all(), f"max err {err.max().item():.3e}"
+    # no rotation: plain LayerNorm
+    q0, _ = torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, None, None, 16, True, True)
+    t = x[0]
+    y = (t - t.mean(-1, keepdim=True)) / torch.sqrt(t.var(-1, unbiased=False, keepdim=True) + 1e-5)
+    y = y * ln_w[0].cpu().double() + ln_b[0].cpu().double()
+    assert (q0.cpu().double() - y).abs().max().item() < 1e-4

@@ -157,6 +157,37 @@ def test_merge_empty_is_a_no_op():
     assert _merge(S=0) == _native.GPA_OK
 
 
+def _qk(**kw):
+    args = dict(qkv=FAKE, B=1, N=10, H=2, D=64, sb=3840, sn=384, koff=128, w=FAKE, b=FAKE,
+                eps=1e-5, pos=FAKE, period=5, cs=FAKE, npos=8, q=FAKE, qd=1, k=FAKE, kd=0,
+                stream=None)
+    args.update(kw)
+    return _native.lib().gpa_qk_norm_rope_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(N=-1), _native.GPA_E_INVALID),
+    (dict(D=128), _native.GPA_E_UNSUPPORTED),
+    (dict(w=None), _native.GPA_E_INVALID),
+    (dict(q=None), _native.GPA_E_INVALID),
+    (dict(cs=None), _native.GPA_E_INVALID),                 # rotation without a table
+    (dict(period=0), _native.GPA_E_INVALID),
+    (dict(npos=0), _native.GPA_E_INVALID),
+    (dict(qd=2), _native.GPA_E_UNSUPPORTED),                # fp16 output
+    (dict(sn=380), _native.GPA_E_INVALID),                  # misaligned row stride
+    (dict(koff=64), _native.GPA_E_INVALID),                 # k overlapping q
+    (dict(qkv=FAKE + 8), _native.GPA_E_INVALID),            # misaligned base
+])
+def test_qk_norm_rope_argument_errors(kw, code):
+    assert _qk(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_qk_norm_rope_empty_is_a_no_op():
+    assert _qk(B=0) == _native.GPA_OK
+    assert _qk(N=0, pos=None, cs=None) == _native.GPA_OK
+
+
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
     (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
     (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
