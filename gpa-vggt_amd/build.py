@@ -45,6 +45,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  The attention kernel keeps its MFMA accumulators
+# in VGPRs with the VGPR form of MFMA selected (195 VGPRs, no AGPR copies or
+# spills at two waves per SIMD).
+FILE_FLAGS = {
+    "attn_keybias.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -54,7 +62,7 @@ def _hipcc() -> str:
 
 def _compile(src: Path, report: bool) -> tuple[Path, str]:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if report:
         cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
     res = subprocess.run(cmd, capture_output=True, text=True)

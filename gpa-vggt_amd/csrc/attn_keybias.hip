@@ -45,16 +45,20 @@
 //     row max and, where it is above m + kTau, rescale (a rare, wave-uniform
 //     branch).  The result is the same softmax; only the (arbitrary) offset
 //     differs from the reference's running max.
-//   * Row sums add up the bf16 P the P.V product uses, with v_dot2_f32_bf16
-//     (exact fp32 sums of bf16 pairs, half the VALU work of fp32 adds), so O
-//     is normalised by exactly the weights it was built from.  The
-//     log-sum-exp therefore is log2 of the sum of the bf16-rounded
-//     probabilities; against the fp32 sum of the reference kernel
-//     (fused_attention.py:113) every term differs by at most 2^-8 relative
-//     (bf16 has 8 significant bits), so the LSE differs by at most
-//     2^-8 / ln 2 < 5.7e-3.  In exchange, two calls over a key partition
-//     combined by their LSE give exactly the normalisation of one call over
-//     all keys, since the outputs are normalised by the same sums.
+//   * Row sums add up the bf16 P the P.V product uses, on the matrix pipe:
+//     v_mfma_f32_4x4x4_16b_bf16 with an all-ones A operand adds each lane's
+//     four B values into its fp32 accumulator (four per block and tile).
+//     The VALU is the busier unit of this kernel, and v_dot2_f32_bf16, the
+//     other way to sum bf16 pairs, does not overlap an in-flight MFMA on
+//     gfx950 (measured: 32 dot2 beside 16 MFMAs of 32x32x16 cost more than
+//     running the two one after the other; fp32 adds, FMAs and the bf16
+//     packing overlap it at ~95-98 %).  O is normalised by exactly the
+//     weights it was built from, so two calls over a key partition combined
+//     by their LSE give exactly the normalisation of one call over all keys.
+//     The log-sum-exp is log2 of the sum of the bf16-rounded probabilities;
+//     against the fp32 sum of the reference kernel (fused_attention.py:113)
+//     every term differs by at most 2^-8 relative, so the LSE differs by at
+//     most 2^-8 / ln 2 < 5.7e-3.
 //   * LDS layouts are XOR-swizzled in 16-byte chunks so that the fragment
 //     reads are free of bank conflicts under both 32- and 64-bank models;
 //     the DMA lanes pick their global chunk so the swizzle costs nothing.
@@ -290,6 +294,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
   const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
   const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
+  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
 
   auto issue = [&](int t, Tile& T) {
     const uint32_t n0 = (uint32_t)t * kKT;
@@ -324,19 +329,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
     v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
   }
 
-  float m_run[kBlk], l_run[kBlk], m_fix[kBlk];
+  float m_run[kBlk], m_fix[kBlk];
+  f32x4 l_acc[kBlk];
   f32x16 o_acc[kBlk][2];
   // Row bound c*(|q| max|k| + max bias/sm_scale) over all keys.
   const float row_k = p.bounds[2 * bh], row_b = p.bounds[2 * bh + 1];
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
     m_run[j] = kMInit;
-    l_run[j] = 0.f;
+    l_acc[j] = f32x4{};
     o_acc[j][0] = f32x16{};
     o_acc[j][1] = f32x16{};
     m_fix[j] = __builtin_fmaf(q_norm[j], row_k, row_b);
   }
-  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 
   // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t for
   // both query blocks, wait until tile t+1 has landed, synchronise.  The
@@ -426,7 +431,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
           const float m_new = ms > m_run[j] + kTau ? ms : m_run[j];
           const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
           m_run[j] = m_new;
-          l_run[j] *= alpha;
+          l_acc[j] *= alpha;
           o_acc[j][0] *= alpha;
           o_acc[j][1] *= alpha;
         }
@@ -435,12 +440,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
 
     // P = 2^(s*c - m) in bf16, row sums, then O^T += V^T . P^T; the V^T
     // operand of k-step s covers the keys whose probabilities this lane
-    // holds in its score registers 8s..8s+7.
+    // holds in its score registers 8s..8s+7.  The row sums of the bf16 P
+    // run on the matrix pipe: a 4x4x4 MFMA with an all-ones A operand adds
+    // each lane's four B values into its accumulator.
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
       const float neg_m = -m_run[j];
       bf16x8 pb[2];
-      float lsum = 0.f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
 #pragma unroll
@@ -451,10 +457,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
           const bf16x2 pv = {(__bf16)p0, (__bf16)p1};
           pb[half][e] = pv[0];
           pb[half][e + 1] = pv[1];
-          lsum = __builtin_amdgcn_fdot2_f32_bf16(pv, ones2, lsum, false);
         }
+        const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
+        const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
+        l_acc[j] = mfma4x4x4(ones4, lo, l_acc[j]);
+        l_acc[j] = mfma4x4x4(ones4, up, l_acc[j]);
       }
-      l_run[j] += lsum;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -502,7 +510,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
     const int64_t row = q_base + 32 * j;
-    const float l_tot = sum_halves(l_run[j]);
+    const float l_tot = sum_halves(l_acc[j][0]);
     const float inv = 1.0f / l_tot;
     if (row < p.M) {
 #pragma unroll
