@@ -11,15 +11,18 @@
 // 32 values bias/sm_scale (-inf past N) and the tile's score bound below.
 //
 // Mapping onto CDNA4
-//   * A workgroup owns 256 queries of one (batch, head): 8 waves of 32
-//     queries, <= 128 VGPRs each, so four waves share a SIMD and the
-//     hardware overlaps one wave's MFMAs with another's softmax.
-//   * K, V and the tile records stream through a 4-slot LDS ring of 32-key
-//     tiles filled by buffer_load ... lds (DMA into LDS, no staging
-//     registers) three tiles ahead of the one being computed.  Keeping
-//     three tiles (24 KB) in flight per workgroup is what hides the L2/HBM
-//     latency: one tile in flight capped the kernel at the latency-bound
-//     rate regardless of its arithmetic.
+//   * A workgroup owns 256 queries of one (batch, head): 4 waves of two
+//     32-query blocks, <= 256 VGPRs each, so two workgroups share a CU (two
+//     waves per SIMD).  Each K or V fragment read from LDS serves both of a
+//     wave's blocks.
+//   * Two passes.  The main pass (attn_main_kernel) runs every wave with a
+//     fixed softmax offset certified on tile 0 and software-pipelines its
+//     tiles (see there); the rare waves it cannot certify are recomputed by
+//     the repair pass (attn_repair_kernel) with a lazily moved offset.
+//   * K, V and the tile records stream through an LDS ring of 32-key tiles
+//     filled by buffer_load ... lds (DMA into LDS, no staging registers)
+//     several tiles ahead of the one being computed; keeping three tiles in
+//     flight per workgroup is what hides the L2/HBM latency.
 //   * Scores are computed transposed, S^T = K . Q^T, on
 //     v_mfma_f32_32x32x16_bf16: a lane owns one query and 16 of the tile's
 //     32 keys (the other 16 sit in lane^32), so the running max, the sum and
@@ -231,13 +234,11 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// LAZY = false: the main pass.  Every wave uses the fixed offset when tile 0
-// certifies it; a wave that cannot certify it stores nothing and sets its
-// flag.  LAZY = true: the repair pass.  Workgroups without a flagged wave
-// exit at once; the others recompute their rows with the lazily moved
-// offset, and the flagged waves store theirs.
-template <bool LAZY>
-__global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
+// The repair pass, for the waves the main pass (attn_main_kernel below) could
+// not certify.  Workgroups without a flagged wave exit at once; the others
+// recompute their rows with a lazily moved offset, and the flagged waves
+// store theirs.
+__global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
   // Four separate LDS objects (not one array) so the compiler's LDS-DMA
   // tracking can tell which slot a DMA writes and which a read reads.
   __shared__ Tile ring0, ring1, ring2, ring3;
@@ -249,12 +250,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
   const int bh = blockIdx.y;
   const int64_t b = bh / p.H, h = bh % p.H;
   uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
-  bool store = true;
-  if constexpr (LAZY) {
-    const uint32_t f = *reinterpret_cast<const uint32_t*>(flag_row);
-    if (f == 0) return;  // workgroup-uniform: before any barrier or DMA
-    store = ((f >> (8 * wave)) & 0xff) != 0;
-  }
+  const uint32_t flags4 = *reinterpret_cast<const uint32_t*>(flag_row);
+  if (flags4 == 0) return;  // workgroup-uniform: before any barrier or DMA
+  const bool store = ((flags4 >> (8 * wave)) & 0xff) != 0;
   const int64_t q_base = (int64_t)blockIdx.x * kQPerWG + wave * kQPerWave + l32;
   const float c = p.c;
 
@@ -329,38 +327,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
     v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
   }
 
-  float m_run[kBlk], m_fix[kBlk];
+  float m_run[kBlk];
   f32x4 l_acc[kBlk];
   f32x16 o_acc[kBlk][2];
-  // Row bound c*(|q| max|k| + max bias/sm_scale) over all keys.
-  const float row_k = p.bounds[2 * bh], row_b = p.bounds[2 * bh + 1];
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
     m_run[j] = kMInit;
     l_acc[j] = f32x4{};
     o_acc[j][0] = f32x16{};
     o_acc[j][1] = f32x16{};
-    m_fix[j] = __builtin_fmaf(q_norm[j], row_k, row_b);
   }
 
   // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t for
   // both query blocks, wait until tile t+1 has landed, synchronise.  The
-  // offset m is chosen in one of three ways (kFirst for tile 0, then kFixed
-  // or kLazy for the rest of the wave's rows):
-  //   kFirst  main pass: m = m_fix when tile 0's exact row max certifies
-  //           that m_fix is within kGap of every row max of the wave (m_fix
-  //           >= every score, and the row max >= tile 0's max); then the
-  //           probabilities of the keys that matter, 2^(x-m) with x within
-  //           ~30 of the row max, stay far above fp32's normal range limit
-  //           2^-126, and the remaining tiles need no max at all.  Repair
-  //           pass: m = tile 0's max.
-  //   kFixed  no max, no rescale, no branch.
-  //   kLazy   x <= c*(|q| max|k| + max bias/sm_scale) over the tile; only
-  //           when that bound exceeds m + kTau can 2^(x-m) leave [0, 2^kTau]:
-  //           then take the exact row max and move m where it is above
-  //           m + kTau, rescaling what has been accumulated.
-  constexpr int kFirst = 0, kFixed = 1, kLazy = 2;
-  bool fixed = false;
+  // offset m starts at tile 0's row max (kFirst) and then moves lazily
+  // (kLazy): x <= c*(|q| max|k| + max bias/sm_scale) over the tile; only
+  // when that bound exceeds m + kTau can 2^(x-m) leave [0, 2^kTau]: then
+  // take the exact row max and move m where it is above m + kTau, rescaling
+  // what has been accumulated.
+  constexpr int kFirst = 0, kLazy = 2;
   auto step = [&](auto mode, const int t, const Tile& T, Tile& Tfree) {
     constexpr int MODE = decltype(mode)::value;
     issue(t + kAhead, Tfree);
@@ -408,18 +393,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
       return max_halves(mx) * c;
     };
     if constexpr (MODE == kFirst) {
-      bool bad = false;
 #pragma unroll
-      for (int j = 0; j < kBlk; ++j) {
-        const float ms = tile_max(sv[j]);
-        if constexpr (LAZY) {
-          m_run[j] = fmaxf(ms, kMInit);
-        } else {
-          bad = bad || !(m_fix[j] - ms <= kGap);
-          m_run[j] = m_fix[j];
-        }
-      }
-      if constexpr (!LAZY) fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+      for (int j = 0; j < kBlk; ++j) m_run[j] = fmaxf(tile_max(sv[j]), kMInit);
     } else if constexpr (MODE == kLazy) {
       // (One branch level per block: nested ones make the register
       // allocator copy the O accumulators on every tile.)
@@ -494,13 +469,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
     if (t < ntiles) step(mode, t++, ring2, ring1);
     if (t < ntiles) step(mode, t++, ring3, ring2);
   };
-  if constexpr (LAZY) {
-    run(std::integral_constant<int, kLazy>{});
-  } else {
-    run(std::integral_constant<int, kFixed>{});
-    store = fixed;
-    if (lane == 0) flag_row[wave] = fixed ? 0 : 1;
-  }
+  run(std::integral_constant<int, kLazy>{});
   // Drain the DMAs still in flight before the workgroup can exit.
   wait_vm<0>();
 
@@ -526,6 +495,283 @@ __global__ __launch_bounds__(kThreads, 2) void attn_keybias_kernel(AttnArgs p) {
         }
       if (p.lse && hi == 0)
         p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_run[j] + __log2f(l_tot);
+    }
+  }
+}
+
+// The main pass: the fixed softmax offset, software-pipelined by one tile.
+//
+// On gfx950 a wave's MFMAs overlap its own VALU work well (measured: 16
+// MFMAs of 32x32x16 interleaved with a tile's softmax in one wave run at
+// ~78 % of the MFMA rate) but another wave's only weakly (~40 % when one
+// wave on a SIMD issues the MFMAs and another the VALU work).  So each
+// iteration t gives the wave independent work for both units:
+//   MFMA  S(t+1) = K(t+1).Q^T + bias(t+1) for both query blocks (8), then
+//         O += V(t)^T . P(t) per block as its P is ready (8), and the row
+//         sums of P(t) (8 small 4x4x4 MFMAs)
+//   VALU  P(t) = 2^(S(t) c - m) in bf16 (32 FMA + 32 exp + 16 packs)
+// and sched_group_barrier interleaves them, one MFMA to three VALU
+// instructions, after the iteration's LDS reads.  Only the last block's
+// P.V product has no VALU work beside it.
+//
+// The offset is the fixed one: m = c*(|q| max|k| + max bias/sm_scale) over
+// all keys (Cauchy-Schwarz), certified per wave on tile 0 (every row max is
+// within kGap of m, so the keys that matter keep probabilities far above
+// fp32's normal range).  A wave that cannot certify it stores nothing and
+// sets its flag for the repair pass.
+//
+// Five ring slots keep tile t (V), tile t+1 (K, bias) and the three tiles
+// in flight; the DMA of tile t+4 refills the slot of tile t-1.  Every wave
+// issues the record DMA (64 lanes x 16 bytes, so a slot's record area is
+// 1 KB, of which the first 144 bytes are the record): wave 0 into the slot,
+// the others into a scratch area nobody reads, so no wave-dependent branch
+// splits an iteration.  The unrolled iterations then form one basic block,
+// in which the pure arithmetic of an iteration could float down to its
+// consumers in the next one; an empty asm that takes the iteration's
+// results as operands keeps it inside.  250 VGPRs, two waves per SIMD.
+constexpr int kMainSlots = 5;
+constexpr int kMainAhead = kMainSlots - 1;  // tiles issued ahead of the one being softmaxed
+
+struct alignas(16) MainTile {
+  uint16_t k[kKT * kHD];
+  uint16_t v[kKT * kHD];
+  float rec[256];
+};
+
+__global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
+  __shared__ MainTile ring0, ring1, ring2, ring3, ring4;
+  __shared__ float rec_sink[256];
+  MainTile* const ring[kMainSlots] = {&ring0, &ring1, &ring2, &ring3, &ring4};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, hi = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.y;
+  const int64_t b = bh / p.H, h = bh % p.H;
+  uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
+  const int64_t q_base = (int64_t)blockIdx.x * kQPerWG + wave * kQPerWave + l32;
+  const float c = p.c;
+  const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
+  const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
+  const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
+
+  // Q^T as the B-operand of S^T = K . Q^T (as in the repair pass).
+  bf16x8 qf[kBlk][4];
+  float q_norm[kBlk];
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    const int64_t row = q_base + 32 * j;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
+                            : bf16x8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)qf[j][ks][e], (float)qf[j][ks][e], ss);
+    }
+    q_norm[j] = __builtin_sqrtf(sum_halves(ss));
+  }
+
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
+  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(R, p.rec_bytes);
+  const uint32_t k_row = (uint32_t)p.k_sn * 2u, v_row = (uint32_t)p.v_sn * 2u;
+  const int slot = wave * 64 + lane;
+  const int s_key = slot >> 3, s_pc = slot & 7;
+  const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
+  const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
+  const uint32_t rec_voff = wave == 0 ? (uint32_t)lane * 16u : 0u;
+  const int ntiles = (int)((p.N + kKT - 1) / kKT);
+  auto issue = [&](int t, MainTile& T) {
+    const uint32_t n0 = (uint32_t)t * kKT;
+    dma16(krs, &T.k[wave * 512], k_voff, n0 * k_row);
+    dma16(vrs, &T.v[wave * 512], v_voff, n0 * v_row);
+    float* dst = wave == 0 ? &T.rec[0] : &rec_sink[0];   // wave-uniform M0, no branch
+    dma16(rrs, dst, rec_voff, (uint32_t)t * (kRec * 4));
+  };
+  // A tile has landed once at most the DMAs of the NT tiles issued after it
+  // (three instructions per tile) are outstanding.
+  auto wait_tiles = [&](auto nt) {
+    constexpr int NT = decltype(nt)::value;
+    wait_vm<3 * NT>();
+  };
+
+  int k_off[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) k_off[ks] = l32 * kHD + (k_chunk(l32, 2 * ks + hi) << 3);
+  int v_base[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db) {
+    const int key = 4 * hi + ((lane & 15) >> 2);
+    const int a = lane & 3;
+    const int ch = db * 4 + ((lane >> 4) & 1) * 2 + (a >> 1);
+    v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
+  }
+
+  float m_off[kBlk];
+  f32x4 l_acc[kBlk];
+  f32x16 o_acc[kBlk][2];
+  const float row_k = p.bounds[2 * bh], row_b = p.bounds[2 * bh + 1];
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    l_acc[j] = f32x4{};
+    o_acc[j][0] = f32x16{};
+    o_acc[j][1] = f32x16{};
+    m_off[j] = __builtin_fmaf(q_norm[j], row_k, row_b);
+  }
+
+  // S(T) for both blocks; the accumulators start from the keys' bias values.
+  auto scores = [&](const MainTile& T, f32x16 (&sv)[kBlk]) {
+    f32x16 bias16;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.rec[8 * g + 4 * hi]);
+      bias16[4 * g + 0] = bv[0];
+      bias16[4 * g + 1] = bv[1];
+      bias16[4 * g + 2] = bv[2];
+      bias16[4 * g + 3] = bv[3];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]);
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) sv[j] = mfma32x32x16(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
+    }
+  };
+  // V^T fragments of a tile (shared by both blocks).
+  auto read_v = [&](const MainTile& T, bf16x8 (&vf)[2][2]) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        typedef short i16x4 __attribute__((ext_vector_type(4)));
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s]);
+        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s + 512]);
+        const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
+        vf[db][s] = bf16x8{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
+      }
+  };
+  // P = 2^(S c - m) of one block in bf16, its row sums, then O += V^T . P.
+  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+  auto softmax_pv = [&](const f32x16& sv, int j, const bf16x8 (&vf)[2][2]) {
+    const float neg_m = -m_off[j];
+    bf16x8 pb[2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
+        const bf16x2 pv2 = {(__bf16)p0, (__bf16)p1};
+        pb[half][e] = pv2[0];
+        pb[half][e + 1] = pv2[1];
+      }
+      const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
+      const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
+      l_acc[j] = mfma4x4x4(ones4, lo, l_acc[j]);
+      l_acc[j] = mfma4x4x4(ones4, up, l_acc[j]);
+    }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) o_acc[j][db] = mfma32x32x16(vf[db][s], pb[s], o_acc[j][db]);
+  };
+
+  f32x16 s_cur[kBlk], s_nxt[kBlk];
+  auto pin_iteration = [&]() {
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      asm volatile("" : "+v"(s_nxt[j]), "+v"(l_acc[j]));
+      asm volatile("" : "+v"(o_acc[j][0]), "+v"(o_acc[j][1]));
+    }
+  };
+
+  // Prologue: tiles 0 .. kMainAhead-1 in flight; S(0) and the certification.
+#pragma unroll
+  for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+  wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
+  tile_barrier();
+  scores(*ring[0], s_cur);
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    float mx = fmaxf(fmaxf(s_cur[j][0], s_cur[j][1]), s_cur[j][2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s_cur[j][r]), s_cur[j][r + 1]);
+    mx = fmaxf(mx, s_cur[j][15]);
+    bad = bad || !(m_off[j] - max_halves(mx) * c <= kGap);
+  }
+  const bool fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+  wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+  tile_barrier();
+
+  // Iteration t: refill the slot of tile t-1 with tile t+kMainAhead; S(t+1)
+  // beside the softmax of S(t); P.V of tile t; tile t+2 lands by its end.
+  // (For t = ntiles-1 the S of the tile past the end is computed from
+  // zero-filled K and records and never used.)
+  auto iter = [&](const int t, const MainTile& Tcur, const MainTile& Tnext, MainTile& Tissue) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(t + kMainAhead, Tissue);
+    scores(Tnext, s_nxt);
+    bf16x8 vf[2][2];
+    read_v(Tcur, vf);
+    softmax_pv(s_cur[0], 0, vf);
+    softmax_pv(s_cur[1], 1, vf);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);   // the 16 LDS reads first
+#pragma unroll
+    for (int i = 0; i < 24; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+    }
+    pin_iteration();
+    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    tile_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) s_cur[j] = s_nxt[j];
+  };
+  // Unrolled by the ring size, so every slot is a compile-time LDS object
+  // (the waitcnt pass can then tell a slot being read from one being filled).
+  int t = 0;
+  for (; t + kMainSlots <= ntiles; t += kMainSlots) {
+#pragma unroll
+    for (int u = 0; u < kMainSlots; ++u)
+      iter(t + u, *ring[u], *ring[(u + 1) % kMainSlots], *ring[(u + kMainAhead) % kMainSlots]);
+  }
+#pragma unroll
+  for (int u = 0; u < kMainSlots - 1; ++u)
+    if (t < ntiles) {
+      iter(t, *ring[u], *ring[(u + 1) % kMainSlots], *ring[(u + kMainAhead) % kMainSlots]);
+      ++t;
+    }
+  if (lane == 0) flag_row[wave] = fixed ? 0 : 1;
+  // Drain the DMAs still in flight before the workgroup can exit.
+  wait_vm<0>();
+  if (!fixed) return;
+
+  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    const int64_t row = q_base + 32 * j;
+    const float l_tot = sum_halves(l_acc[j][0]);
+    const float inv = 1.0f / l_tot;
+    if (row < p.M) {
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = db * 32 + 8 * g + 4 * hi;
+          const bf16x4 ov = {(__bf16)(o_acc[j][db][4 * g + 0] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 1] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 2] * inv),
+                             (__bf16)(o_acc[j][db][4 * g + 3] * inv)};
+          *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
+        }
+      if (p.lse && hi == 0)
+        p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_off[j] + __log2f(l_tot);
     }
   }
 }
@@ -608,7 +854,7 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   const int64_t gx = (M + kQPerWG - 1) / kQPerWG;
   // Buffer offsets are 32-bit: one (batch, head) slice of K and V, plus the
   // tiles fetched past its end, must stay below 2^31 bytes.
-  const int64_t span = N + (kAhead + 1) * kKT;
+  const int64_t span = N + (kMainAhead + 1) * kKT;
   if (gx > 0x7fffffff || span * k_sn * 2 >= ((int64_t)1 << 31) ||
       span * v_sn * 2 >= ((int64_t)1 << 31)) {
     gpa_set_error("gpa_attn_keybias_bf16: one head's K/V slice exceeds 2 GiB");
@@ -679,8 +925,8 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   p.c = c;
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
-  hipLaunchKernelGGL(attn_keybias_kernel<false>, grid, block, 0, s, p);
-  hipLaunchKernelGGL(attn_keybias_kernel<true>, grid, block, 0, s, p);
+  hipLaunchKernelGGL(attn_main_kernel, grid, block, 0, s, p);
+  hipLaunchKernelGGL(attn_repair_kernel, grid, block, 0, s, p);
   e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("gpa_attn_keybias_bf16: launch failed: %s", hipGetErrorString(e));
