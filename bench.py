@@ -330,7 +330,7 @@ def main(argv=None) -> int:
             traffic = None
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic, "kernel": "attn_keybias_kernel",
+                "traffic": traffic, "kernel": "attn_main_kernel",
                 "flops_per_launch": f_attn}
 
     e2e = None

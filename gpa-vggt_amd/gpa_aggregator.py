@@ -367,8 +367,20 @@ class DinoV2Reg(nn.Module):
         self.norm = nn.LayerNorm(dim, eps=1e-6)
         self.nreg = cfg.num_register_tokens
 
+    def patchify(self, img: torch.Tensor) -> torch.Tensor:
+        """The stride-14 14x14 convolution as what it is, one GEMM over the
+        non-overlapping patches (MIOpen runs this conv shape with its naive
+        direct kernel, ~120 ms at 200 frames).  [B, 3, H, W] -> [B, P, D]."""
+        B, C, H, W = img.shape
+        ps = self.patch.kernel_size[0]
+        gh, gw = H // ps, W // ps
+        cols = (img[:, :, :gh * ps, :gw * ps].reshape(B, C, gh, ps, gw, ps)
+                .permute(0, 2, 4, 1, 3, 5).reshape(B * gh * gw, C * ps * ps))
+        w = self.patch.weight.reshape(self.patch.out_channels, C * ps * ps)
+        return F.linear(cols, w, self.patch.bias).view(B, gh * gw, -1)
+
     def forward(self, img: torch.Tensor) -> torch.Tensor:
-        x = self.patch(img).flatten(2).transpose(1, 2)
+        x = self.patchify(img)
         x = torch.cat((self.cls_token.expand(x.shape[0], -1, -1).to(x.dtype), x), dim=1)
         x = x + self.pos_embed.to(x.dtype)
         x = torch.cat((x[:, :1], self.register_tokens.expand(x.shape[0], -1, -1).to(x.dtype),

@@ -130,6 +130,20 @@ def test_embed_token_layout_without_vit_blocks():
     assert torch.equal(tok[0, 1:5], model.register_token[0, 0])
 
 
+def test_patchify_equals_the_strided_convolution():
+    cfg = A.GpaConfig(vit_depth=0, depth=1, img_size=56)
+    emb = A.DinoV2Reg(cfg)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        emb.patch.weight.copy_(torch.randn(emb.patch.weight.shape, generator=g) * 0.05)
+        emb.patch.bias.copy_(torch.randn(emb.patch.bias.shape, generator=g))
+        img = torch.rand(2, 3, 56, 56, generator=g)
+        want = emb.patch(img).flatten(2).transpose(1, 2)
+        got = emb.patchify(img)
+    assert got.shape == want.shape == (2, 16, 1024)
+    assert torch.allclose(got, want, atol=1e-4, rtol=1e-4)
+
+
 def test_aggregator_flops_closed_form():
     cfg = A.GpaConfig()
     f = A.aggregator_flops(cfg, 200)
