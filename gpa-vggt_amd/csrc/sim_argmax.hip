@@ -27,6 +27,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace gpa {
 namespace {
 
@@ -37,6 +39,14 @@ constexpr int kTN = 64;  // destination rows per LDS stage
 // above, which keeps the kernel within the VGPR budget of two waves/SIMD.
 __host__ __device__ constexpr int src_blocks(int ks) { return ks <= 4 ? 4 : 2; }
 __host__ __device__ constexpr int rows_per_wg(int ks) { return kWaves * src_blocks(ks) * 16; }
+
+// Wait until at most N vector-memory instructions of this wave are in flight
+// (lgkm and export counters untouched).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 struct SimArgs {
   const uint16_t* a;
@@ -249,6 +259,224 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
   }
 }
 
+
+// D = 128 (the model's 128-d projected metric): the same work decomposition,
+// software-pipelined.  Destination tiles of 16 rows (4 KB) arrive by
+// buffer_load ... lds DMA into an 8-slot ring (each wave copies a quarter of
+// a tile with one instruction; the lane picks the global chunk that lands in
+// its swizzled LDS position).  Iteration i runs the 32 MFMAs of tiles
+// 2i+2, 2i+3 beside the max/argmax epilogue of tiles 2i, 2i+1, whose scores
+// the previous iteration produced, interleaved one MFMA to three VALU
+// instructions; the MFMA and the VALU unit of a wave then overlap instead of
+// taking turns.  One barrier per iteration recycles the slots of the tiles
+// just read; tiles past the split end read as zeros and are masked in the
+// last epilogue.
+constexpr int kPipeRing = 8;                 // 16-row tile slots
+constexpr int kPipePairsAhead = kPipeRing / 2 - 1;
+
+__global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
+  constexpr int KS = 4, kSB = 4, D = 128;
+  constexpr int kRowsPerWG = rows_per_wg(KS);
+  constexpr int TILE_BYTES = 16 * D * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t r0[TILE_BYTES], r1[TILE_BYTES], r2[TILE_BYTES],
+      r3[TILE_BYTES], r4[TILE_BYTES], r5[TILE_BYTES], r6[TILE_BYTES], r7[TILE_BYTES];
+  uint8_t* const ring[kPipeRing] = {r0, r1, r2, r3, r4, r5, r6, r7};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int quad = lane >> 4, l16 = lane & 15;
+  const int64_t batch = blockIdx.y;
+  int mblock, split;
+  map_block(p, blockIdx.x, mblock, split);
+  const int64_t m_wg = (int64_t)mblock * kRowsPerWG;
+  if (m_wg >= p.M) return;
+
+  const int64_t n_begin = (int64_t)split * p.n_chunk;
+  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
+  const uint16_t* A = p.a + batch * p.a_sb;
+  const uint16_t* Bm = p.b + batch * p.b_sb;
+
+  bf16x8 sf[kSB][KS];
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb) {
+    const int64_t row = m_wg + wave * (kSB * 16) + sb * 16 + l16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      sf[sb][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(A + row * p.a_sm + ks * 32 + quad * 8)
+                             : bf16x8{};
+  }
+
+  float best[kSB][4];
+  int bt[kSB][4];
+  const int tile0 = (int)(n_begin >> 4);
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      best[sb][r] = -INFINITY;
+      bt[sb][r] = tile0;
+    }
+
+  const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + 15) / 16) : 0;
+  const int npairs = (ntiles + 1) / 2;
+  const uint32_t b_row = (uint32_t)p.b_sn * 2u;
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(
+      Bm + n_begin * p.b_sn,
+      n_end > n_begin ? (uint32_t)(((n_end - n_begin - 1) * p.b_sn + D) * 2) : 0u);
+  // DMA role: wave w fills rows 4w..4w+3 of a tile; lane l lands at LDS
+  // chunk l%16 of row 4w + l/16 and fetches the global chunk the XOR
+  // swizzle (chunk ^ row) puts there.
+  const int d_row = 4 * wave + (lane >> 4), d_ch = (lane & 15) ^ d_row;
+  const uint32_t d_voff = (uint32_t)d_row * b_row + d_ch * 16;
+  auto issue = [&](int tile, uint8_t* T) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        brs, (__attribute__((address_space(3))) void*)(T + wave * 1024), 16, d_voff,
+        (uint32_t)tile * 16u * b_row, 0, 0);
+  };
+  // A-operand reads: row l16 of the tile, logical chunk 4ks + quad.
+  int a_off[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) a_off[ks] = l16 * (D * 2) + (((4 * ks + quad) ^ l16) << 4);
+
+  auto mfma_tile = [&](const uint8_t* T, f32x4 (&acc)[kSB]) {
+#pragma unroll
+    for (int sb = 0; sb < kSB; ++sb) acc[sb] = f32x4{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 af = *reinterpret_cast<const bf16x8*>(T + a_off[ks]);
+#pragma unroll
+      for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32(af, sf[sb][ks], acc[sb]);
+    }
+  };
+  // Running max / first tile reaching it, per slot (strict >: an earlier
+  // tile keeps a tie).  MASKED: rows at or past the split end never win.
+  auto epilogue = [&](const f32x4 (&acc)[kSB], int tile_rel, auto masked) {
+    const int tile = tile0 + tile_rel;
+#pragma unroll
+    for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = acc[sb][r];
+        bool upd = v > best[sb][r];
+        if constexpr (decltype(masked)::value)
+          upd = upd && (n_begin + (int64_t)tile_rel * 16 + 4 * quad + r < n_end);
+        best[sb][r] = upd ? v : best[sb][r];
+        bt[sb][r] = upd ? tile : bt[sb][r];
+      }
+  };
+
+  f32x4 cur[2][kSB], nxt[2][kSB];
+  auto pin = [&]() {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int sb = 0; sb < kSB; ++sb) asm volatile("" : "+v"(nxt[u][sb]));
+#pragma unroll
+    for (int sb = 0; sb < kSB; ++sb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(best[sb][r]), "+v"(bt[sb][r]));
+  };
+
+  if (npairs > 0) {
+    // Prologue: pairs 0 .. kPipePairsAhead-1 in flight; scores of pair 0.
+#pragma unroll
+    for (int i = 0; i < kPipePairsAhead; ++i) {
+      issue(2 * i, ring[2 * i]);
+      issue(2 * i + 1, ring[2 * i + 1]);
+    }
+    wait_vm<2 * (kPipePairsAhead - 1)>();
+    __syncthreads();
+    mfma_tile(ring[0], cur[0]);
+    mfma_tile(ring[1], cur[1]);
+    wait_vm<2 * (kPipePairsAhead - 2)>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // Iteration i: fetch pair i+3 into the slots of pair i-1 (read by
+    // iteration i-2); scores of pair i+1 beside the epilogue of pair i
+    // (scored by iteration i-1); pair i+2 lands by its end.
+    auto iter = [&](const int i, const uint8_t* Ta, const uint8_t* Tb, uint8_t* Ia, uint8_t* Ib) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(2 * (i + kPipePairsAhead), Ia);
+      issue(2 * (i + kPipePairsAhead) + 1, Ib);
+      mfma_tile(Ta, nxt[0]);
+      mfma_tile(Tb, nxt[1]);
+      epilogue(cur[0], 2 * i, std::false_type{});
+      epilogue(cur[1], 2 * i + 1, std::false_type{});
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+      pin();
+      wait_vm<2 * (kPipePairsAhead - 2)>();
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sb = 0; sb < kSB; ++sb) {
+        cur[0][sb] = nxt[0][sb];
+        cur[1][sb] = nxt[1][sb];
+      }
+    };
+    // Pair j sits in slots 2(j mod 4), 2(j mod 4)+1; iteration i reads pair
+    // i+1 and fills the slots of pair i+3 = i-1 (mod 4).
+    int i = 0;
+    for (; i + 4 <= npairs - 1; i += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rd = (u + 1) % 4, wr = (u + 3) % 4;
+        iter(i + u, ring[2 * rd], ring[2 * rd + 1], ring[2 * wr], ring[2 * wr + 1]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+      if (i < npairs - 1) {
+        const int rd = (u + 1) % 4, wr = (u + 3) % 4;
+        iter(i, ring[2 * rd], ring[2 * rd + 1], ring[2 * wr], ring[2 * wr + 1]);
+        ++i;
+      }
+    // The last pair, masked against the split end.
+    epilogue(cur[0], 2 * (npairs - 1), std::true_type{});
+    epilogue(cur[1], 2 * (npairs - 1) + 1, std::true_type{});
+    wait_vm<0>();
+  }
+
+#pragma unroll
+  for (int sb = 0; sb < kSB; ++sb) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = best[sb][r];
+      const int idx = bt[sb][r] * 16 + 4 * quad + r;
+      const bool take = v > bv || (v == bv && idx < bi);
+      bv = take ? v : bv;
+      bi = take ? idx : bi;
+    }
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float ov = __shfl_xor(bv, sh);
+      const int oi = __shfl_xor(bi, sh);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    const int64_t m = m_wg + wave * (kSB * 16) + sb * 16 + l16;
+    if (quad == 0 && m < p.M) {
+      if (p.splits == 1) {
+        p.out_max[batch * p.omax_sb + m] = bv;
+        p.out_idx[batch * p.oidx_sb + m] = bi;
+      } else {
+        const int64_t o = (batch * p.splits + split) * p.M + m;
+        p.part_max[o] = bv;
+        p.part_idx[o] = bi;
+      }
+    }
+  }
+}
+
 // Merge per-split partials in split order; strict `>` keeps the earlier
 // split (lower destination indices) on ties.
 __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_t B) {
@@ -352,9 +580,10 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   }
 
   const SimPlan pl = make_plan(B, M, N, D);
-  // Buffer offsets are 32-bit: one split of destination rows (plus a stage
-  // of overrun) must stay below 2^31 bytes.
-  if ((pl.n_chunk + kTN) * b_sn * 2 >= ((int64_t)1 << 31)) {
+  // Buffer offsets are 32-bit: one split of destination rows, plus the
+  // tiles fetched past its end (two stages, or eight 16-row tiles), must
+  // stay below 2^31 bytes.
+  if ((pl.n_chunk + 2 * kTN) * b_sn * 2 >= ((int64_t)1 << 31)) {
     gpa_set_error("gpa_sim_argmax_bf16: destination split exceeds 2 GiB (N=%lld, row stride %lld)",
                   (long long)N, (long long)b_sn);
     return GPA_E_UNSUPPORTED;
@@ -394,7 +623,8 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   switch (D / 32) {
 #define GPA_SIM_CASE(ks) \
   case ks: hipLaunchKernelGGL(sim_argmax_kernel<ks>, grid, block, 0, s, p); break;
-    GPA_SIM_CASE(1) GPA_SIM_CASE(2) GPA_SIM_CASE(3) GPA_SIM_CASE(4)
+    case 4: hipLaunchKernelGGL(sim_argmax_d128_kernel, grid, block, 0, s, p); break;
+    GPA_SIM_CASE(1) GPA_SIM_CASE(2) GPA_SIM_CASE(3)
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
