@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Four kernels sit behind this boundary:
+ * Five entry points (and their kernels) sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
