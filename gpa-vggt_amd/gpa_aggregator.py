@@ -16,7 +16,8 @@ merging kernels sit in:
     vggt/layers/rope.py:167-209);
   * the GPA schedule of aggregator.py:133-150 and :317-325: global blocks
     below `early_frame_split` run frame attention plus the shared K/V set
-    (vggt/layers/attention.py:73-176, split path), global blocks in
+    (vggt/layers/attention.py:73-176, split path; the pooled summaries by
+    the `gpa::pool_shared` kernel), global blocks in
     [merging, merge_end] merge K/V (attention.py:233-268) at `merge_ratio`,
     the core blocks at `core_merge_ratio`.
 
@@ -284,7 +285,8 @@ class GpaAttention(nn.Module):
         del own_k, own_v
         kp = self.cfg.broadcast_pool
         if kp > 0:
-            pooled_k, pooled_v, pool_size, _ = pool_shared(k5, v5, pts, g, kp)
+            pooled_k, pooled_v, pool_size, _ = torch.ops.gpa.pool_shared(
+                k, v, S, pts, g, kp, False)
             sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
             sh_v = torch.cat([v5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_v], dim=2)
             bias = torch.zeros(B, H, 1, sh_k.shape[2], device=q.device, dtype=torch.float32)
@@ -299,8 +301,10 @@ class GpaAttention(nn.Module):
         return combine_by_lse(out_a, lse_a, out_b, lse_b, S)
 
 
-def pool_shared(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid: int, kp: int):
-    """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140).
+def pool_shared_torch(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid: int, kp: int):
+    """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140),
+    restated with torch ops; the harness runs the `gpa::pool_shared` kernel,
+    and this restatement pins it in the tests.
 
     k5/v5 [B, H, S, P, D].  Seeds are the stride-kp lattice patches; every
     patch joins the seed whose key it matches best by cosine (per head), and

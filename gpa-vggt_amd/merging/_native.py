@@ -16,6 +16,9 @@ two custom ops:
     gpa::qk_norm_rope(Tensor qkv, Tensor ln_w, Tensor ln_b, float eps,
                       Tensor? pos, Tensor? rope_cs, int heads, bool q_f32,
                       bool k_f32) -> (Tensor q, Tensor k)
+    gpa::pool_shared(Tensor k, Tensor v, int frames, int pts, int grid, int kp,
+                     bool want_assign) -> (Tensor pk, Tensor pv, Tensor size,
+                                           Tensor assign)
 
 All launch on torch's current stream of the input's device.  There is no
 fallback: a missing library or a non-GPU tensor raises.
@@ -30,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -102,6 +105,13 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_int, _vp, ctypes.c_int,  # q_out, q_dtype, k_out, k_dtype
         _vp,                           # stream
     ]
+    lib.gpa_pool_shared_bf16.restype = ctypes.c_int
+    lib.gpa_pool_shared_bf16.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, _vp,  # k, v, pooled_k, pooled_v, size, assign
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # B, H, S, P, pts, grid, kp, D
+        _i64, _i64, _i64, _i64, _i64, _i64,  # k strides, v strides
+        _vp,                           # stream
+    ]
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -137,7 +147,8 @@ def lib() -> ctypes.CDLL:
 def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
-            "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16")
+            "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
+            "gpa_pool_shared_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -463,3 +474,53 @@ def _qk_norm_rope_fake(qkv, ln_w, ln_b, eps, pos, rope_cs, heads, q_f32, k_f32):
     B, N, _ = qkv.shape
     return (qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if q_f32 else torch.bfloat16),
             qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if k_f32 else torch.bfloat16))
+
+
+@torch.library.custom_op("gpa::pool_shared", mutates_args=())
+def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: int, kp: int,
+                want_assign: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Pooled summaries of the frame-special shared set from k, v [B, H, S*P, 64]
+    (bf16): returns pooled k, v [B, H, S*npool, 64] bf16, size [B, H, S, npool]
+    fp32 and, if asked, the assignment [B, H, S, grid*grid] int32 (else empty)."""
+    dev = _require_gpu(k, v)
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16 or t.dim() != 4:
+            raise ValueError(f"gpa::pool_shared: {name} must be bf16 [B,H,N,64], got {t.dtype} "
+                             f"{tuple(t.shape)}")
+    if k.shape != v.shape:
+        raise ValueError(f"gpa::pool_shared: k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    B, H, N, D = k.shape
+    S = int(frames)
+    if S <= 0 or N % S != 0:
+        raise ValueError(f"gpa::pool_shared: {N} tokens do not split into {S} frames")
+    P = N // S
+    nh = -(-int(grid) // int(kp)) if kp > 0 else 0
+    npool = nh * nh
+    if not _rows_ok(k, 8):
+        k = k.contiguous()
+    if v.stride(-1) != 1 or v.data_ptr() % 4 or any(st % 2 for st in v.stride()[:-1]):
+        v = v.contiguous()
+    pk = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
+    pv = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
+    size = torch.empty(B, H, S, npool, device=dev, dtype=torch.float32)
+    assign = (torch.empty(B, H, S, grid * grid, device=dev, dtype=torch.int32) if want_assign
+              else torch.empty(0, device=dev, dtype=torch.int32))
+    if pk.numel() == 0:
+        return pk, pv, size, assign
+    with torch.cuda.device(dev):
+        rc = lib().gpa_pool_shared_bf16(
+            k.data_ptr(), v.data_ptr(), pk.data_ptr(), pv.data_ptr(), size.data_ptr(),
+            assign.data_ptr() if want_assign else None, B, H, S, P, pts, grid, kp, D,
+            _st(k, 0), _st(k, 1), _rs(k, 2), _st(v, 0), _st(v, 1), _rs(v, 2), _stream(dev))
+    _check(rc, "gpa::pool_shared")
+    return pk, pv, size, assign
+
+
+@pool_shared.register_fake
+def _pool_shared_fake(k, v, frames, pts, grid, kp, want_assign):
+    B, H, N, D = k.shape
+    nh = -(-grid // kp)
+    npool = nh * nh
+    return (k.new_empty(B, H, frames * npool, D), k.new_empty(B, H, frames * npool, D),
+            k.new_empty(B, H, frames, npool, dtype=torch.float32),
+            k.new_empty((B, H, frames, grid * grid) if want_assign else (0,), dtype=torch.int32))

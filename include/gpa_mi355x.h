@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Five entry points (and their kernels) sit behind this boundary:
+ * Six entry points (and their kernels) sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -18,6 +18,8 @@
  *   gpa_qk_norm_rope_bf16 — qk LayerNorm + 2D RoPE + cast of a block's
  *                           attention operands (replaces the torch op
  *                           sequence of vggt/layers/attention.py:210-220).
+ *   gpa_pool_shared_bf16  — pooled summaries of the frame-special shared
+ *                           K/V set (replaces vggt/layers/attention.py:113-140).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -41,7 +43,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 4
+#define GPA_ABI_VERSION 5
 
 enum {
   GPA_OK = 0,
@@ -191,6 +193,33 @@ int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H, int6
                           const int32_t* pos, int64_t period,
                           const float* rope_cs, int64_t npos,
                           void* q_out, int q_dtype, void* k_out, int k_dtype, void* stream);
+
+/*
+ * Pooled summaries of the frame-special shared K/V set.  For every
+ * (b, h, frame s) and its patch keys x_p = k[b, h, s*P + pts + p, :]
+ * (p < grid*grid, D = 64):
+ *   seeds y_g: the patches (gy*kp, gx*kp) of the grid, g = gy*nh + gx,
+ *              nh = ceil(grid/kp), npool = nh*nh (<= 64)
+ *   assign a_p = argmax_g bf16(bf16(x_p/max(|x_p|,1e-6)) . bf16(y_g/max(|y_g|,1e-6)))
+ *              (fp32 dots rounded to bf16; the lowest g wins ties)
+ *   size[b,h,s,g]         = #{p : a_p = g}                                (fp32)
+ *   pooled_k[b,h,s*npool+g,:] = sum_{a_p=g} k_p / max(size, 1)           (bf16)
+ *   pooled_v likewise from v (same token positions).
+ * pooled_k / pooled_v are contiguous [B, H, S*npool, 64], size [B, H, S, npool];
+ * assign (nullable) receives a_p as int32 [B, H, S, grid*grid].  k rows
+ * 16-byte aligned, v rows 4-byte aligned, unit feature stride.  The sums
+ * are fp32 atomics, so the last bits of a mean may differ between runs, as
+ * with the reference's scatter_add_.
+ * Replaces `_pool` of vggt/layers/attention.py:113-140 (the einsum at :130
+ * under bf16 autocast) and the pool sizes behind the bias of :142-146; the
+ * reference module interface has no such entry point (it runs these as
+ * torch ops).
+ */
+int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* pooled_v,
+                         float* size, int32_t* assign, int64_t B, int64_t H, int64_t S,
+                         int64_t P, int64_t pts, int64_t grid, int64_t kp, int64_t D,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                         int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream);
 
 #ifdef __cplusplus
 }

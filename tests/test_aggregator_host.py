@@ -94,7 +94,7 @@ def test_pool_shared_matches_bruteforce():
     B, H, S, pts, grid, kp, D = 1, 2, 3, 5, 7, 3, 16
     k5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
     v5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
-    pk, pv, size, assign = A.pool_shared(k5, v5, pts, grid, kp)
+    pk, pv, size, assign = A.pool_shared_torch(k5, v5, pts, grid, kp)
     bpk, bpv, bsize, bassign = _pool_bruteforce(k5, v5, pts, grid, kp)
     npool = 9
     assert np.array_equal(assign.numpy(), bassign)

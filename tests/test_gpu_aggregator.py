@@ -146,12 +146,11 @@ def test_frame_special_block_attention_matches_reference(dev):
         got = blk.attn(xn, rope, None)
         # the device's pool assignment, from the module's own K/V
         _, kd, vd = blk.attn.qk(xn, rope)
-        _, _, size_d, assign_d = A.pool_shared(kd.view(1, 16, FRAMES, P, 64),
-                                               vd.reshape(1, 16, FRAMES, P, 64), PTS, GRID, 8)
+        _, _, size_d, assign_d = torch.ops.gpa.pool_shared(kd, vd, FRAMES, PTS, GRID, 8, True)
     q, k, v = _qkv_ref(blk, xn, pos)
     q16, k16, v16 = q.bfloat16().float(), k.bfloat16().float(), v
     k5, v5 = k16.view(1, 16, FRAMES, P, 64), v16.view(1, 16, FRAMES, P, 64)
-    assign = assign_d.cpu()
+    assign = assign_d.cpu().long()
     npool = 25
     onehot = F.one_hot(assign, npool).double()                     # [1,16,S,1369,25]
     cnt = onehot.sum(3)                                            # [1,16,S,25]
@@ -222,3 +221,55 @@ def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32):
     y = (t - t.mean(-1, keepdim=True)) / torch.sqrt(t.var(-1, unbiased=False, keepdim=True) + 1e-5)
     y = y * ln_w[0].cpu().double() + ln_b[0].cpu().double()
     assert (q0.cpu().double() - y).abs().max().item() < 1e-4
+
+
+def _pool_bf16_fp64(x: torch.Tensor, grid: int, kp: int):
+    """fp64 scores of bf16-rounded normalised rows against bf16-rounded
+    normalised seeds (the einsum of attention.py:130 under bf16 autocast,
+    before its own bf16 rounding): x [G, grid*grid, 64] -> [G, grid*grid, npool]."""
+    def nb(t):
+        t = t.float()
+        return (t / t.norm(dim=-1, keepdim=True).clamp_min(1e-6)).bfloat16().double()
+    G = x.shape[0]
+    seeds = x.view(G, grid, grid, 64)[:, ::kp, ::kp].reshape(G, -1, 64)
+    return torch.einsum("gpd,gsd->gps", nb(x), nb(seeds))
+
+
+@pytest.mark.parametrize("kp", [8, 5])
+def test_pool_shared_kernel_matches_reference(dev, kp):
+    """gpa::pool_shared against the scores in fp64 (assignment, except rows
+    whose best two scores are within two bf16 steps, where the bf16 rounding
+    of the reference's scores decides) and, given its own assignment, exact
+    sizes and fp64 means of the K and V rows."""
+    g = torch.Generator(device=dev).manual_seed(kp)
+    B, H, S = 1, 4, 3
+    k = (torch.randn(B, H, S * P, 64, generator=g, device=dev) * 0.7).bfloat16()
+    v = torch.randn(B, H, S * P, 64, generator=g, device=dev).bfloat16()
+    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, GRID, kp, True)
+    nh = -(-GRID // kp)
+    npool = nh * nh
+    assert pk.shape == (B, H, S * npool, 64) and size.shape == (B, H, S, npool)
+    kp5 = k.view(B, H, S, P, 64)[:, :, :, PTS:].reshape(-1, GRID * GRID, 64).cpu()
+    vp5 = v.view(B, H, S, P, 64)[:, :, :, PTS:].reshape(-1, GRID * GRID, 64).cpu()
+    sc = _pool_bf16_fp64(kp5, GRID, kp)
+    top2 = sc.topk(2, dim=-1).values
+    sure = (top2[..., 0] - top2[..., 1]) > 2 * 2.0 ** -8
+    a = assign.cpu().long().reshape(-1, GRID * GRID)
+    assert torch.equal(a[sure], sc.argmax(-1)[sure])
+    assert sure.float().mean() > 0.5
+    # seeds belong to their own group
+    seeds_pos = [(y * GRID + x) for y in range(0, GRID, kp) for x in range(0, GRID, kp)]
+    assert torch.equal(a[:, seeds_pos], torch.arange(npool).expand(a.shape[0], npool))
+    onehot = torch.nn.functional.one_hot(a, npool).double()          # [G, p, npool]
+    cnt = onehot.sum(1)
+    assert torch.equal(size.cpu().reshape(-1, npool).double(), cnt)
+    mk = torch.einsum("gps,gpd->gsd", onehot, kp5.double()) / cnt.clamp_min(1)[..., None]
+    mv = torch.einsum("gps,gpd->gsd", onehot, vp5.double()) / cnt.clamp_min(1)[..., None]
+    for got, want in ((pk, mk), (pv, mv)):
+        got = got.cpu().double().reshape(-1, npool, 64)
+        err = (got - want).abs()
+        assert (err <= 2.0 ** -8 * want.abs() + 1e-6).all(), f"max err {err.max().item():.3e}"
+    # the torch restatement on the same device agrees on the sure rows
+    _, _, _, a_t = A.pool_shared_torch(k.view(B, H, S, P, 64), v.view(B, H, S, P, 64),
+                                       PTS, GRID, kp)
+    assert torch.equal(a_t.cpu().reshape(-1, GRID * GRID)[sure], a[sure])

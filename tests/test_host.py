@@ -188,6 +188,35 @@ def test_qk_norm_rope_empty_is_a_no_op():
     assert _qk(N=0, pos=None, cs=None) == _native.GPA_OK
 
 
+def _pool(**kw):
+    args = dict(k=FAKE, v=FAKE, pk=FAKE, pv=FAKE, size=FAKE, assign=None, B=1, H=2, S=3, P=1374,
+                pts=5, grid=37, kp=8, D=64, ksb=0, ksh=263808, ksn=64, vsb=0, vsh=263808, vsn=64,
+                stream=None)
+    args.update(kw)
+    return _native.lib().gpa_pool_shared_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(S=-1), _native.GPA_E_INVALID),
+    (dict(kp=0), _native.GPA_E_INVALID),
+    (dict(D=128), _native.GPA_E_UNSUPPORTED),
+    (dict(k=None), _native.GPA_E_INVALID),
+    (dict(size=None), _native.GPA_E_INVALID),
+    (dict(P=1000), _native.GPA_E_INVALID),                  # frame too short for the grid
+    (dict(kp=4), _native.GPA_E_UNSUPPORTED),                # 100 seeds > 64
+    (dict(ksn=60), _native.GPA_E_INVALID),                  # misaligned k rows
+    (dict(vsn=63), _native.GPA_E_INVALID),                  # misaligned v rows
+])
+def test_pool_shared_argument_errors(kw, code):
+    assert _pool(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_pool_shared_empty_is_a_no_op():
+    assert _pool(B=0) == _native.GPA_OK
+    assert _pool(S=0) == _native.GPA_OK
+
+
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
     (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
     (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
