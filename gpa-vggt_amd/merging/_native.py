@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -112,6 +112,13 @@ def _bind(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64, _i64, _i64,  # k strides, v strides
         _vp,                           # stream
     ]
+    lib.gpa_merge_metric_bf16.restype = ctypes.c_int
+    lib.gpa_merge_metric_bf16.argtypes = [
+        _vp, ctypes.c_int,             # metric, metric dtype
+        _i64, _i64, _i64, _i64, _i64,  # B, N, C, metric strides (b, n)
+        _vp, _i64, _vp, ctypes.c_int,  # proj, P, order, norm_mode
+        _vp, _vp,                      # out, stream
+    ]
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -148,7 +155,7 @@ def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
-            "gpa_pool_shared_bf16")
+            "gpa_pool_shared_bf16", "gpa_merge_metric_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -524,3 +531,54 @@ def _pool_shared_fake(k, v, frames, pts, grid, kp, want_assign):
     return (k.new_empty(B, H, frames * npool, D), k.new_empty(B, H, frames * npool, D),
             k.new_empty(B, H, frames, npool, dtype=torch.float32),
             k.new_empty((B, H, frames, grid * grid) if want_assign else (0,), dtype=torch.int32))
+
+
+# --------------------------------------------------------------------------
+# gpa::merge_metric
+# --------------------------------------------------------------------------
+
+_METRIC_DTYPES = {torch.float32: GPA_DTYPE_F32, torch.bfloat16: GPA_DTYPE_BF16}
+
+
+@torch.library.custom_op("gpa::merge_metric", mutates_args=())
+def merge_metric(metric: torch.Tensor, proj: torch.Tensor, order: Optional[torch.Tensor],
+                 norm_bf16: bool) -> torch.Tensor:
+    """bf16(normalise(bf16(bf16(metric[:, order]) @ proj))) as [B, N, 128] bf16.
+
+    metric [B, N, C] fp32 or bf16 (C in 256, 512, 768, 1024), proj [C, 128]
+    bf16, order [N] int64 token positions (None: identity).  norm_bf16 rounds
+    the row norm to bf16 before the division (the chain without autocast)."""
+    dev = _require_gpu(metric, proj)
+    if metric.dim() != 3 or metric.dtype not in _METRIC_DTYPES:
+        raise ValueError(f"gpa::merge_metric: metric must be fp32/bf16 [B,N,C], got "
+                         f"{metric.dtype} {tuple(metric.shape)}")
+    B, N, C = metric.shape
+    if proj.dtype != torch.bfloat16 or proj.dim() != 2 or proj.shape[0] != C:
+        raise ValueError(f"gpa::merge_metric: proj must be bf16 [{C}, P], got {proj.dtype} "
+                         f"{tuple(proj.shape)}")
+    P = proj.shape[1]
+    proj = proj.contiguous()
+    if order is not None:
+        _require_gpu(order)
+        if order.dtype != torch.int64 or order.shape != (N,):
+            raise ValueError(f"gpa::merge_metric: order must be int64 [{N}], got {order.dtype} "
+                             f"{tuple(order.shape)}")
+        order = order.contiguous()
+    if not _rows_ok(metric, 16 // metric.element_size()):
+        metric = metric.contiguous()
+    out = torch.empty(B, N, P, device=dev, dtype=torch.bfloat16)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(dev):
+        rc = lib().gpa_merge_metric_bf16(
+            metric.data_ptr(), _METRIC_DTYPES[metric.dtype], B, N, C, _st(metric, 0),
+            _rs(metric, 1), proj.data_ptr(), P, None if order is None else order.data_ptr(),
+            1 if norm_bf16 else 0, out.data_ptr(), _stream(dev))
+    _check(rc, "gpa::merge_metric")
+    return out
+
+
+@merge_metric.register_fake
+def _merge_metric_fake(metric, proj, order, norm_bf16):
+    B, N, _ = metric.shape
+    return metric.new_empty(B, N, proj.shape[1], dtype=torch.bfloat16)

@@ -14,6 +14,14 @@ Orderings the reference leaves to torch's sort are fixed here:
 These are the orders torch's GPU radix sort produces for such inputs.
 `merge.index` exposes the index tensors for inspection.
 
+Under bf16 autocast (the model's case), or on a bf16 metric, the metric
+projection, normalisation, dst/src split and bf16 cast (reference :180-187
+and fused_similarity.py:90-95) run as one gfx950 kernel
+(`gpa::merge_metric`) that writes the similarity operands [dst | src]
+directly; node_max keeps the dtype the reference's division yields (fp32
+under autocast).  Other chains (fp32 arithmetic without autocast, no
+projection) keep the torch ops on the device.
+
 `merge` and `merge.heads` in "sum" / "mean" mode (fp32, bf16, fp16 rows)
 run the deterministic gfx950 merge kernel (`gpa::merge_heads`): every
 output slot lists its own token and the tokens merged into it once per
@@ -87,6 +95,38 @@ def dst_mask(num_imgs: int, w: int, h: int, sx: int, sy: int, num_special: int,
     return mask
 
 
+_PROJ_CACHE: dict = {}
+
+
+def _projection(dev: torch.device, C: int, metric_dim: int,
+                dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The fixed Gaussian basis of the metric projection (reference
+    merging/merge.py:181-184: `randn(C, metric_dim)` from a device generator
+    seeded with PROJ_SEED), drawn once per device and shape and kept."""
+    key = (dev, C, metric_dim, dtype)
+    proj = _PROJ_CACHE.get(key)
+    if proj is None:
+        g_proj = torch.Generator(device=dev)
+        g_proj.manual_seed(PROJ_SEED)
+        proj = torch.randn(C, metric_dim, device=dev, dtype=torch.float32,
+                           generator=g_proj).to(dtype)
+        _PROJ_CACHE[key] = proj
+    return proj
+
+
+def _front_end_mode(metric: torch.Tensor, C: int, metric_dim: int) -> Optional[str]:
+    """Which rounding chain the fused front end reproduces, or None when the
+    reference's chain is one the kernel does not compute (no projection, a
+    projection other than C -> 128, fp32 arithmetic without autocast, fp16)."""
+    if metric_dim != 128 or C not in (256, 512, 768, 1024):
+        return None
+    if torch.is_autocast_enabled("cuda"):
+        if torch.get_autocast_dtype("cuda") != torch.bfloat16:
+            return None
+        return "autocast" if metric.dtype in (torch.float32, torch.bfloat16) else None
+    return "bf16" if metric.dtype == torch.bfloat16 else None
+
+
 def token_merge_bipartite2d(
     metric: torch.Tensor,
     w: int,
@@ -132,21 +172,34 @@ def token_merge_bipartite2d(
         a_pos = order[num_dst:]
         num_src = N - num_dst
 
-        if metric_dim and metric_dim < C:
-            g_proj = torch.Generator(device=dev)
-            g_proj.manual_seed(PROJ_SEED)
-            proj = torch.randn(C, metric_dim, device=dev, dtype=torch.float32,
-                               generator=g_proj).to(metric.dtype)
-            metric = metric @ proj
-        metric = metric / metric.norm(dim=-1, keepdim=True)
-        a = metric.index_select(1, a_pos)
-        b = metric.index_select(1, b_pos)
+        front = _front_end_mode(metric, C, metric_dim)
+        if front is not None:
+            # One kernel: projection, normalisation, [dst | src] split and
+            # bf16 cast (reference :180-187 plus the cast of
+            # fused_similarity.py:90-95); node_max keeps the dtype the
+            # reference's division produces.
+            ab = _native.merge_metric(metric, _projection(dev, C, metric_dim), order,
+                                      front == "bf16")
+            max_dtype = torch.float32 if front == "autocast" else torch.bfloat16
+            a = ab[:, num_dst:]
+            b = ab[:, :num_dst]
+        else:
+            if metric_dim and metric_dim < C:
+                proj = _projection(dev, C, metric_dim, torch.float32).to(metric.dtype)
+                metric = metric @ proj
+            metric = metric / metric.norm(dim=-1, keepdim=True)
+            a = metric.index_select(1, a_pos)
+            b = metric.index_select(1, b_pos)
+            max_dtype = metric.dtype
 
         r = min(num_src, r)
-        if num_src > 0:
+        if num_src > 0 and front is not None:
+            node_max, node_idx = torch.ops.gpa.sim_argmax(a, b)     # fp32 row max
+            node_max = node_max.to(max_dtype)
+        elif num_src > 0:
             node_max, node_idx = fused_similarity_argmax(a, b)
         else:
-            node_max = metric.new_empty(B, 0)
+            node_max = torch.empty(B, 0, device=dev, dtype=max_dtype)
             node_idx = torch.empty(B, 0, device=dev, dtype=torch.int64)
         edge = torch.argsort(node_max, dim=-1, descending=True, stable=True)
         src_rank = edge[:, :r]          # merged source rows (rows of `a`)

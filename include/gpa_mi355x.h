@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Six entry points (and their kernels) sit behind this boundary:
+ * Seven entry points (and their kernels) sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -20,6 +20,8 @@
  *                           sequence of vggt/layers/attention.py:210-220).
  *   gpa_pool_shared_bf16  — pooled summaries of the frame-special shared
  *                           K/V set (replaces vggt/layers/attention.py:113-140).
+ *   gpa_merge_metric_bf16 — the merge's metric projection, normalisation and
+ *                           dst/src split (replaces merging/merge.py:180-187).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -43,7 +45,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 5
+#define GPA_ABI_VERSION 6
 
 enum {
   GPA_OK = 0,
@@ -220,6 +222,27 @@ int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* poo
                          int64_t P, int64_t pts, int64_t grid, int64_t kp, int64_t D,
                          int64_t k_sb, int64_t k_sh, int64_t k_sn,
                          int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream);
+
+/*
+ * Front end of the bipartite merge: for every batch b and output row j,
+ * with t = order[j] (order == NULL: t = j),
+ *   y = bf16( bf16(metric[b, t, :]) @ proj )   C -> P, fp32 accumulation
+ *   n = sqrt(sum y^2) in fp32; norm_mode 1 rounds n to bf16
+ *   out[b, j, :] = bf16(y / n)                  (no epsilon: a zero row gives NaN)
+ * metric: [B, N, C] of metric_dtype (GPA_DTYPE_F32 or GPA_DTYPE_BF16), unit
+ * feature stride, 16-byte aligned rows, C in {256, 512, 768, 1024}; proj:
+ * contiguous [C][P] bf16, P = 128; order: int64 [N]; out: contiguous
+ * [B, N, P] bf16.  With order = [dst positions | src positions] the output
+ * holds the similarity operands b then a.
+ * Replaces merging/merge.py:180-187 as it runs under bf16 autocast
+ * (norm_mode 0: `metric @ proj` in bf16, the norm in fp32, the division
+ * promoted to fp32, then the bf16 cast of fused_similarity.py:90-95) or on
+ * a bf16 metric without autocast (norm_mode 1); the reference runs it as
+ * torch ops (projection, norm, division, two index gathers).
+ */
+int gpa_merge_metric_bf16(const void* metric, int metric_dtype, int64_t B, int64_t N, int64_t C,
+                          int64_t m_sb, int64_t m_sn, const void* proj, int64_t P,
+                          const int64_t* order, int norm_mode, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -217,6 +217,33 @@ def test_pool_shared_empty_is_a_no_op():
     assert _pool(S=0) == _native.GPA_OK
 
 
+def _metric(**kw):
+    args = dict(x=FAKE, dt=_native.GPA_DTYPE_F32, B=1, N=5496, C=1024, sb=0, sn=1024, proj=FAKE,
+                P=128, order=None, mode=0, out=FAKE, stream=None)
+    args.update(kw)
+    return _native.lib().gpa_merge_metric_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(N=-1), _native.GPA_E_INVALID),
+    (dict(dt=2), _native.GPA_E_UNSUPPORTED),                # fp16 metric
+    (dict(mode=2), _native.GPA_E_INVALID),
+    (dict(C=1000, sn=1000), _native.GPA_E_UNSUPPORTED),     # C not in {256, 512, 768, 1024}
+    (dict(P=64), _native.GPA_E_UNSUPPORTED),
+    (dict(x=None), _native.GPA_E_INVALID),
+    (dict(out=None), _native.GPA_E_INVALID),
+    (dict(sn=1020), _native.GPA_E_INVALID),                 # rows not 16-byte aligned
+])
+def test_merge_metric_argument_errors(kw, code):
+    assert _metric(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_merge_metric_empty_is_a_no_op():
+    assert _metric(B=0) == _native.GPA_OK
+    assert _metric(N=0) == _native.GPA_OK
+
+
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
     (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
     (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
