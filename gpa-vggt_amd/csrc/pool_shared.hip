@@ -13,15 +13,23 @@
 // autocast: the normalised keys and seeds enter the einsum (:130) in bf16,
 // its scores come back in bf16, argmax takes the first maximum, and the
 // sums run in fp32 (scatter_add_, :132-139) before the cast back.  The
-// reference's torch path sums with atomics in a run-dependent order; here
-// the sums are fp32 LDS atomics too (the group's rows into 64-float
-// accumulators per seed), so the last bits of a mean can differ between
-// runs exactly as the reference's do.
+// reference sums with atomics in a run-dependent order; here every sum has
+// a single owner and a fixed order, so the means are deterministic.
 //
-// One workgroup (4 waves) per group: the seeds go to LDS, each thread
-// assigns rows (64 FMAs per seed, seeds read as LDS broadcasts), then every
-// wave adds two rows at a time (lane = feature pair) into the accumulators.
-// HBM-bound: K read twice (the second read hits L2), V once.
+// One workgroup (4 waves) per group; both steps run on MFMA
+// (v_mfma_f32_32x32x16_bf16).
+//   Assignment: the normalised seeds are the A operands (one or two blocks
+//   of 32 seeds, held in registers), each 32-row tile of normalised patch
+//   keys the B operand; a lane's 16 scores of a row are rounded to bf16 and
+//   reduced with the partner lane (lowest seed on ties).  The assignment
+//   bytes go to LDS.
+//   Sums: a one-hot GEMM, D[seed][feature] = sum_rows [a_row == seed] x,
+//   exact bf16 products summed in fp32.  Wave w owns one tensor (K or V) and
+//   one feature half over every tile: its raw rows are staged in an LDS tile
+//   and read back transposed as the B operand (rows along k), the A operand
+//   is built from the assignment bytes, and the means go straight from the
+//   accumulators to the output.
+// HBM-bound: K read twice (the second pass mostly from L2), V once.
 #include "gpa_common.h"
 
 #include <math.h>
@@ -30,6 +38,7 @@ namespace gpa {
 namespace {
 
 constexpr int kPoolThreads = 256;
+constexpr int kPoolWaves = kPoolThreads / 64;
 constexpr int kPoolD = 64;
 constexpr int kMaxPool = 64;      // seeds per frame (kp >= 5 at grid 37)
 constexpr int kMaxPatches = 4096;
@@ -47,14 +56,18 @@ struct PoolArgs {
 
 __device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
-__global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
-  __shared__ float seed[kMaxPool][kPoolD];          // normalised, bf16-rounded
-  __shared__ float acc_k[kMaxPool][kPoolD];
-  __shared__ float acc_v[kMaxPool][kPoolD];
-  __shared__ int count[kMaxPool];
-  __shared__ uint8_t asg[kMaxPatches];
+// Row stride of a wave's staged tile (32 rows x 32 features), in bf16: 8 of
+// padding, so the transposed reads (lanes = features, the two lane halves 8
+// rows apart) fall in different banks.
+constexpr int kStage = 32 + 8;
 
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
+  __shared__ int count[kMaxPool];
+  __shared__ __attribute__((aligned(16))) uint8_t asg[kMaxPatches];
+  __shared__ __attribute__((aligned(16))) uint16_t stage[kPoolWaves][32][kStage];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
   const int grp = blockIdx.x;                  // (b*H + h)*S + s
   const int s = grp % a.S;
   const int bh = grp / a.S;
@@ -63,86 +76,155 @@ __global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
   const uint16_t* K = a.k + b * a.k_sb + h * a.k_sh + ((int64_t)s * a.P + a.pts) * a.k_sn;
   const uint16_t* Vp = a.v + b * a.v_sb + h * a.v_sh + ((int64_t)s * a.P + a.pts) * a.v_sn;
 
-  // Row p of K as 64 floats; returns |x|^2.
-  auto load_row = [&](int p, float (&x)[kPoolD]) {
-    const bf16x8* r = reinterpret_cast<const bf16x8*>(K + (int64_t)p * a.k_sn);
+  for (int g = tid; g < a.npool; g += kPoolThreads) count[g] = 0;
+
+  // Features 16ks + 8hi .. +8 (ks < 4) of a row: the MFMA operand layout of
+  // a 16-feature k-step.  Lanes l and l^32 share a row.
+  auto load_half = [&](const uint16_t* base, int64_t stride, int p, bf16x8 (&r)[4]) {
+    const uint16_t* row = base + (int64_t)p * stride + 8 * hi;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) r[ks] = *reinterpret_cast<const bf16x8*>(row + 16 * ks);
+  };
+  // x / max(|x|, 1e-6) in fp32, rounded to bf16; both lanes of a row take part.
+  auto normalise = [&](const bf16x8 (&r)[4], bf16x8 (&nb)[4]) {
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < kPoolD / 8; ++c) {
-      const bf16x8 v8 = r[c];
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[8 * c + e] = (float)v8[e];
-        ss = __builtin_fmaf(x[8 * c + e], x[8 * c + e], ss);
-      }
-    }
-    return ss;
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)r[ks][e], (float)r[ks][e], ss);
+    const float inv = 1.0f / fmaxf(__builtin_sqrtf(sum_halves(ss)), 1e-6f);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nb[ks][e] = (__bf16)((float)r[ks][e] * inv);
   };
 
-  for (int i = tid; i < a.npool * kPoolD; i += kPoolThreads) {
-    (&acc_k[0][0])[i] = 0.f;
-    (&acc_v[0][0])[i] = 0.f;
-  }
-  for (int g = tid; g < a.npool; g += kPoolThreads) count[g] = 0;
-  // Seeds: one thread per seed.
-  for (int g = tid; g < a.npool; g += kPoolThreads) {
-    const int gy = g / a.nh, gx = g % a.nh;
-    float x[kPoolD];
-    const float inv = 1.0f / fmaxf(__builtin_sqrtf(load_row(gy * a.kp * a.grid + gx * a.kp, x)), 1e-6f);
+  // Seed blocks: block sb holds seeds 32sb .. 32sb+31 in lane rows l32 (zero
+  // past npool; their scores are masked anyway).
+  const int nsb = (a.npool + 31) / 32;
+  bf16x8 seed[2][4];
 #pragma unroll
-    for (int d = 0; d < kPoolD; ++d) seed[g][d] = bf16_round(x[d] * inv);
+  for (int sb = 0; sb < 2; ++sb) {
+    const int g = sb * 32 + l32;
+    const int gc = g < a.npool ? g : a.npool - 1;
+    const int gy = gc / a.nh, gx = gc % a.nh;
+    bf16x8 r[4];
+    load_half(K, a.k_sn, gy * a.kp * a.grid + gx * a.kp, r);
+    normalise(r, seed[sb]);
+    if (g >= a.npool)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) seed[sb][ks] = bf16x8{};
   }
-  __syncthreads();
+  __syncthreads();                             // counts cleared
 
-  // Assignment: one thread per row.
-  for (int p = tid; p < npatch; p += kPoolThreads) {
-    float x[kPoolD];
-    const float inv = 1.0f / fmaxf(__builtin_sqrtf(load_row(p, x)), 1e-6f);
-#pragma unroll
-    for (int d = 0; d < kPoolD; ++d) x[d] = bf16_round(x[d] * inv);
+  const int ntile = (npatch + 31) / 32;        // ntile * 32 <= kMaxPatches
+  // Assignment: every row's scores against the seeds, rounded to bf16.
+  for (int t = wave; t < ntile; t += kPoolWaves) {
+    const int p = t * 32 + l32;
+    const bool valid = p < npatch;
+    bf16x8 rk[4], xb[4];
+    load_half(K, a.k_sn, valid ? p : npatch - 1, rk);
+    normalise(rk, xb);
     float best = -INFINITY;
-    int bg = 0;
-    for (int g = 0; g < a.npool; ++g) {
-      float dot = 0.f;
+    int bi = 0;
 #pragma unroll
-      for (int d = 0; d < kPoolD; ++d) dot = __builtin_fmaf(x[d], seed[g][d], dot);
-      dot = bf16_round(dot);
-      if (dot > best) {
-        best = dot;
-        bg = g;
+    for (int sb = 0; sb < 2; ++sb) {           // compile-time index into seed[]
+      if (sb >= nsb) break;                    // wave-uniform
+      f32x16 sc = {};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sc = mfma32x32x16(seed[sb][ks], xb[ks], sc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {           // seeds in increasing order
+        const int g = sb * 32 + mfma_row(r, hi);
+        const float v = bf16_round(sc[r]);
+        if (g < a.npool && v > best) {
+          best = v;
+          bi = g;
+        }
       }
     }
-    asg[p] = (uint8_t)bg;
-    atomicAdd(&count[bg], 1);
-    if (a.assign) a.assign[(int64_t)grp * npatch + p] = bg;
+    const float pb = __shfl_xor(best, 32);
+    const int pi = __shfl_xor(bi, 32);
+    if (pb > best || (pb == best && pi < bi)) bi = pi;
+    if (hi == 0) {
+      asg[p] = valid ? (uint8_t)bi : (uint8_t)0xff;   // 0xff matches no seed
+      if (valid) {
+        atomicAdd(&count[bi], 1);
+        if (a.assign) a.assign[(int64_t)grp * npatch + p] = bi;
+      }
+    }
   }
   __syncthreads();
 
-  // Sums: a wave adds two rows per step, lane = (row parity, feature pair).
-  const int lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, fp = (lane & 31) * 2;
-  for (int p = 2 * wave + half; p < npatch; p += 2 * (kPoolThreads / 64)) {
-    const int g = asg[p];
-    const bf16x2 kv = *reinterpret_cast<const bf16x2*>(K + (int64_t)p * a.k_sn + fp);
-    const bf16x2 vv = *reinterpret_cast<const bf16x2*>(Vp + (int64_t)p * a.v_sn + fp);
-    atomicAdd(&acc_k[g][fp], (float)kv[0]);
-    atomicAdd(&acc_k[g][fp + 1], (float)kv[1]);
-    atomicAdd(&acc_v[g][fp], (float)vv[0]);
-    atomicAdd(&acc_v[g][fp + 1], (float)vv[1]);
+  // Sums and means: wave w owns tensor (w >> 1 ? V : K) and feature half
+  // fb = w & 1 over every tile, accumulating the one-hot GEMM
+  //   D[seed][feature] = sum_rows [a_row == seed] x[row][feature]
+  // on MFMA (A = one-hot from the assignment bytes, B = the raw rows, staged
+  // in the wave's LDS tile and read back transposed so rows run along k).
+  // Each (seed, feature) has one owner, so the sums need no atomics and are
+  // deterministic.  The next tile's rows load while this one is multiplied.
+  const bool is_v = wave >> 1;
+  const int fb = wave & 1;
+  const uint16_t* X = is_v ? Vp : K;
+  const int64_t x_sn = is_v ? a.v_sn : a.k_sn;
+  auto load_quarter = [&](int t, bf16x8 (&r)[2]) {
+    const int p = t * 32 + l32;
+    const uint16_t* row = X + (int64_t)(p < npatch ? p : npatch - 1) * x_sn + 32 * fb + 16 * hi;
+    r[0] = *reinterpret_cast<const bf16x8*>(row);
+    r[1] = *reinterpret_cast<const bf16x8*>(row + 8);
+  };
+  f32x16 acc[2] = {};
+  bf16x8 nx[2];
+  load_quarter(0, nx);
+  for (int t = 0; t < ntile; ++t) {
+    const bool valid = t * 32 + l32 < npatch;
+    *reinterpret_cast<bf16x8*>(&stage[wave][l32][16 * hi]) = valid ? nx[0] : bf16x8{};
+    *reinterpret_cast<bf16x8*>(&stage[wave][l32][16 * hi + 8]) = valid ? nx[1] : bf16x8{};
+    load_quarter(t + 1 < ntile ? t + 1 : t, nx);
+    // The wave's own LDS writes above are visible to these reads (in order).
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int r0 = 16 * kk + 8 * hi;         // rows r0 .. r0+7 of the tile
+      const uint2 ab = *reinterpret_cast<const uint2*>(&asg[t * 32 + r0]);
+      u32x4 bx;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bx[q] = (uint32_t)stage[wave][r0 + 2 * q][l32] |
+                ((uint32_t)stage[wave][r0 + 2 * q + 1][l32] << 16);
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        if (sb >= nsb) break;                  // wave-uniform
+        const uint32_t id = (uint32_t)(sb * 32 + l32);
+        u32x4 oh;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = q < 2 ? ab.x : ab.y;
+          const uint32_t b0 = (w >> (16 * (q & 1))) & 0xffu, b1 = (w >> (16 * (q & 1) + 8)) & 0xffu;
+          oh[q] = (b0 == id ? 0x3f80u : 0u) | (b1 == id ? 0x3f800000u : 0u);   // bf16 1.0
+        }
+        acc[sb] = mfma32x32x16(__builtin_bit_cast(bf16x8, oh), __builtin_bit_cast(bf16x8, bx),
+                               acc[sb]);
+      }
+    }
   }
-  __syncthreads();
 
+  // Means straight to the output (counts are complete since the barrier).
   const int64_t out_row0 = ((int64_t)bh * a.S + s) * a.npool;   // row of [B, H, S*npool]
-  for (int i = tid; i < a.npool * kPoolD; i += kPoolThreads) {
-    const int g = i / kPoolD, d = i % kPoolD;
-    const float n = (float)count[g];
-    const float inv = 1.0f / fmaxf(n, 1.0f);
-    const int64_t o = (out_row0 + g) * kPoolD + d;
-    const __bf16 mk = (__bf16)(acc_k[g][d] * inv), mv = (__bf16)(acc_v[g][d] * inv);
-    a.pk[o] = __builtin_bit_cast(uint16_t, mk);
-    a.pv[o] = __builtin_bit_cast(uint16_t, mv);
-    if (d == 0) a.size[out_row0 + g] = n;
+  uint16_t* out = is_v ? a.pv : a.pk;
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    if (sb >= nsb) break;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int g = sb * 32 + mfma_row(r, hi);
+      if (g < a.npool) {
+        const float inv = 1.0f / fmaxf((float)count[g], 1.0f);
+        out[(out_row0 + g) * kPoolD + 32 * fb + l32] =
+            __builtin_bit_cast(uint16_t, (__bf16)(acc[sb][r] * inv));
+      }
+    }
   }
+  for (int g = tid; g < a.npool; g += kPoolThreads) a.size[out_row0 + g] = (float)count[g];
 }
 
 }  // namespace
@@ -181,12 +263,13 @@ extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k
                   (long long)(nh * nh), (long long)(grid * grid));
     return GPA_E_UNSUPPORTED;
   }
-  const bool aligned = (uintptr_t)k % 16 == 0 && (uintptr_t)v % 4 == 0 && (B == 1 || k_sb % 8 == 0) &&
-                       (H == 1 || k_sh % 8 == 0) && k_sn % 8 == 0 && v_sb % 2 == 0 &&
-                       v_sh % 2 == 0 && v_sn % 2 == 0 && k_sn >= D && v_sn >= D;
+  const bool aligned = (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 &&
+                       (B == 1 || (k_sb % 8 == 0 && v_sb % 8 == 0)) &&
+                       (H == 1 || (k_sh % 8 == 0 && v_sh % 8 == 0)) && k_sn % 8 == 0 &&
+                       v_sn % 8 == 0 && k_sn >= D && v_sn >= D;
   if (!aligned) {
-    gpa_set_error("gpa_pool_shared_bf16: k rows must be 16-byte and v rows 4-byte aligned, unit "
-                  "feature stride");
+    gpa_set_error("gpa_pool_shared_bf16: k and v rows must be 16-byte aligned, unit feature "
+                  "stride");
     return GPA_E_INVALID;
   }
   const int64_t groups = B * H * S;

@@ -505,7 +505,7 @@ def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: i
     npool = nh * nh
     if not _rows_ok(k, 8):
         k = k.contiguous()
-    if v.stride(-1) != 1 or v.data_ptr() % 4 or any(st % 2 for st in v.stride()[:-1]):
+    if not _rows_ok(v, 8):
         v = v.contiguous()
     pk = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
     pv = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)

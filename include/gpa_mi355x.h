@@ -208,10 +208,10 @@ int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H, int6
  *   pooled_k[b,h,s*npool+g,:] = sum_{a_p=g} k_p / max(size, 1)           (bf16)
  *   pooled_v likewise from v (same token positions).
  * pooled_k / pooled_v are contiguous [B, H, S*npool, 64], size [B, H, S, npool];
- * assign (nullable) receives a_p as int32 [B, H, S, grid*grid].  k rows
- * 16-byte aligned, v rows 4-byte aligned, unit feature stride.  The sums
- * are fp32 atomics, so the last bits of a mean may differ between runs, as
- * with the reference's scatter_add_.
+ * assign (nullable) receives a_p as int32 [B, H, S, grid*grid].  k and v
+ * rows 16-byte aligned, unit feature stride.  The sums run in fp32 in a
+ * fixed order, so the means are deterministic (the reference's scatter_add_
+ * sums with atomics in a run-dependent order).
  * Replaces `_pool` of vggt/layers/attention.py:113-140 (the einsum at :130
  * under bf16 autocast) and the pool sizes behind the bias of :142-146; the
  * reference module interface has no such entry point (it runs these as

@@ -240,7 +240,8 @@ def test_pool_shared_kernel_matches_reference(dev, kp):
     """gpa::pool_shared against the scores in fp64 (assignment, except rows
     whose best two scores are within two bf16 steps, where the bf16 rounding
     of the reference's scores decides) and, given its own assignment, exact
-    sizes and fp64 means of the K and V rows."""
+    sizes and fp64 means of the K and V rows; bit-identical on a second call
+    and on strided V rows."""
     g = torch.Generator(device=dev).manual_seed(kp)
     B, H, S = 1, 4, 3
     k = (torch.randn(B, H, S * P, 64, generator=g, device=dev) * 0.7).bfloat16()
@@ -273,3 +274,10 @@ def test_pool_shared_kernel_matches_reference(dev, kp):
     _, _, _, a_t = A.pool_shared_torch(k.view(B, H, S, P, 64), v.view(B, H, S, P, 64),
                                        PTS, GRID, kp)
     assert torch.equal(a_t.cpu().reshape(-1, GRID * GRID)[sure], a[sure])
+    # deterministic sums (fixed order), and strided rows give the same result
+    pk2, pv2, size2, _ = torch.ops.gpa.pool_shared(k, v, S, PTS, GRID, kp, False)
+    assert torch.equal(pk2, pk) and torch.equal(pv2, pv) and torch.equal(size2, size)
+    wide = torch.zeros(B, H, S * P, 128, device=dev, dtype=torch.bfloat16)
+    wide[..., 32:96] = v
+    pk3, pv3, _, _ = torch.ops.gpa.pool_shared(k, wide[..., 32:96], S, PTS, GRID, kp, False)
+    assert torch.equal(pk3, pk) and torch.equal(pv3, pv)

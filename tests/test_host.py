@@ -206,6 +206,7 @@ def _pool(**kw):
     (dict(kp=4), _native.GPA_E_UNSUPPORTED),                # 100 seeds > 64
     (dict(ksn=60), _native.GPA_E_INVALID),                  # misaligned k rows
     (dict(vsn=63), _native.GPA_E_INVALID),                  # misaligned v rows
+    (dict(vsn=68), _native.GPA_E_INVALID),                  # v rows not 16-byte aligned
 ])
 def test_pool_shared_argument_errors(kw, code):
     assert _pool(**kw) == code
