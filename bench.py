@@ -319,7 +319,51 @@ def main(argv=None) -> int:
             "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
             "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
         del qs, ks, vs, bs, out_a, lse_a, out_b, lse_b
+        # Row f2: the pooled shared set (kp 8: 25 seeds per frame) at 200 frames.
+        kk = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
+        vv = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
+        fn = lambda: torch.ops.gpa.pool_shared(kk, vv, S, pts, 37, 8, False)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 5))
+        nbytes = 2 * 16 * S * (P - pts) * 64 * 2
+        kernels["pool_shared_200f_16h_kp8"] = {
+            "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+        del kk, vv
+        # Row f3: the merge front end (projection 1024 -> 128, normalise,
+        # [dst | src] gather, bf16) on the fp32 norm1 output of 274,800 tokens.
+        from merging.merge import _projection, dst_mask
+        g = torch.Generator(device=dev)
+        g.manual_seed(33)
+        order = torch.argsort(dst_mask(S, 37, 37, 2, 2, pts, False, g, dev), stable=True)
+        metric = torch.randn(1, S * P, 1024, device=dev)
+        proj = _projection(dev, 1024, 128)
+        fn = lambda: _native.merge_metric(metric, proj, order, False)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 5))
+        nbytes = S * P * (1024 * 4 + 128 * 2)
+        kernels["merge_metric_200f_274800x1024_f32"] = {
+            "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+        del metric, order
         log("[bench] 200-frame shapes done")
+
+    if not args.no_200f:
+        # Row f4: the fp16 twins at the headline shapes (fp16 autocast stack).
+        sh, dh = W.sim_inputs(m=75_000, n=25_000, seed=0, device=dev)
+        sh, dh = sh.half(), dh.half()
+        fn = lambda: fused_similarity_argmax(sh, dh)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 10))
+        kernels["sim_argmax_f16_75000x25000x128"] = kernel_entry(f_sim, t)
+        del sh, dh
+        qh, kh, vh, bh = q.half(), k.half(), v.half(), bias.half()
+        fn = lambda: attention_keybias(qh, kh, vh, bh, SM_SCALE)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 3))
+        kernels["attn_keybias_f16_16h_274800x68700"] = kernel_entry(f_attn, t)
+        del qh, kh, vh, bh
+        log("[bench] fp16 shapes done")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12
     traffic = None

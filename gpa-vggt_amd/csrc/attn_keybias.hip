@@ -83,9 +83,16 @@ constexpr int kKT = 32;                       // keys per tile
 constexpr int kHD = 64;                       // head dim
 constexpr int kRing = 4;                      // LDS tile slots
 constexpr int kAhead = kRing - 1;             // tiles in flight beyond the current one
-constexpr float kTau = 16.0f;                 // lazy rescale threshold (log2): P <= 2^kTau
+// Lazy rescale threshold (log2), P <= 2^kTau: bf16 has fp32's exponent
+// range; fp16's largest value is 65504 < 2^16.
+template <bool F16> constexpr float kTau = F16 ? 15.0f : 16.0f;
 constexpr float kMInit = -1.0e30f;            // finite initial offset (all -inf rows give 0)
-constexpr float kGap = 64.0f;                 // largest offset above the row max a fixed m may have
+// Fixed offset of the main pass: m = bound - kShift, certified when the row
+// max is within kGap of the bound.  bf16 P keeps fp32's exponent range, so
+// the gap may be wide; fp16 P sits in [2^(kShift-kGap), 2^kShift] =
+// [2^-1, 2^15], far from fp16's subnormals and below its 65504.
+template <bool F16> constexpr float kGap = F16 ? 16.0f : 64.0f;
+template <bool F16> constexpr float kShift = F16 ? 15.0f : 0.0f;
 constexpr int kRec = 36;                      // words per tile record
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -160,6 +167,7 @@ __device__ __forceinline__ void wait_vm() {
 
 // Tile records: one thread per key; the 32 lanes of a tile reduce the two
 // maxima with cross-lane shuffles.  Keys past N get bias -inf and |k| = 0.
+template <bool F16>
 __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B*H*ntiles*32
   const bool live = i < a.total_keys;
@@ -172,6 +180,8 @@ __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
       x = static_cast<const float*>(a.bias)[off] * a.mul;
     else if (a.kind == GPA_BIAS_BF16)
       x = bf16_bits_to_f32(static_cast<const uint16_t*>(a.bias)[off]) * a.mul;
+    else if (a.kind == GPA_BIAS_F16)
+      x = (float)static_cast<const _Float16*>(a.bias)[off] * a.mul;
     else
       x = 0.f;
     const bf16x8* kr = reinterpret_cast<const bf16x8*>(a.k + bb * a.k_sb + hb * a.k_sh + n * a.k_sn);
@@ -180,7 +190,10 @@ __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
     for (int j = 0; j < kHD / 8; ++j) {
       const bf16x8 v = kr[j];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)v[e], (float)v[e], ss);
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(v[e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
     }
     kn = __builtin_sqrtf(ss);
   }
@@ -238,6 +251,7 @@ __device__ __forceinline__ void tile_barrier() {
 // not certify.  Workgroups without a flagged wave exit at once; the others
 // recompute their rows with a lazily moved offset, and the flagged waves
 // store theirs.
+template <bool F16>
 __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
   // Four separate LDS objects (not one array) so the compiler's LDS-DMA
   // tracking can tell which slot a DMA writes and which a read reads.
@@ -274,7 +288,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
       qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
                             : bf16x8{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)qf[j][ks][e], (float)qf[j][ks][e], ss);
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(qf[j][ks][e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
     }
     q_norm[j] = __builtin_sqrtf(sum_halves(ss));
   }
@@ -292,7 +309,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
   const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
   const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
-  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+  const __bf16 one = f32_to_half<F16>(1.0f);
+  const bf16x4 ones4 = {one, one, one, one};
 
   auto issue = [&](int t, Tile& T) {
     const uint32_t n0 = (uint32_t)t * kKT;
@@ -367,7 +385,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
     for (int ks = 0; ks < 4; ++ks) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]);
 #pragma unroll
-      for (int j = 0; j < kBlk; ++j) sv[j] = mfma32x32x16(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
+      for (int j = 0; j < kBlk; ++j)
+        sv[j] = mfma32x32x16_t<F16>(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
     }
 
     // V^T fragments of this tile, shared by both blocks.
@@ -401,9 +420,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 #pragma unroll
       for (int j = 0; j < kBlk; ++j) {
         const float ub = __builtin_fmaf(q_norm[j], T.rec[kKT], T.rec[kKT + 1]);
-        if (__builtin_amdgcn_ballot_w64(ub > m_run[j] + kTau) != 0) {
+        if (__builtin_amdgcn_ballot_w64(ub > m_run[j] + kTau<F16>) != 0) {
           const float ms = tile_max(sv[j]);
-          const float m_new = ms > m_run[j] + kTau ? ms : m_run[j];
+          const float m_new = ms > m_run[j] + kTau<F16> ? ms : m_run[j];
           const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
           m_run[j] = m_new;
           l_acc[j] *= alpha;
@@ -429,19 +448,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e], c, neg_m));
           const float p1 =
               __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e + 1], c, neg_m));
-          const bf16x2 pv = {(__bf16)p0, (__bf16)p1};
+          const bf16x2 pv = pack2<F16>(p0, p1);
           pb[half][e] = pv[0];
           pb[half][e + 1] = pv[1];
         }
         const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
         const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
-        l_acc[j] = mfma4x4x4(ones4, lo, l_acc[j]);
-        l_acc[j] = mfma4x4x4(ones4, up, l_acc[j]);
+        l_acc[j] = mfma4x4x4_t<F16>(ones4, lo, l_acc[j]);
+        l_acc[j] = mfma4x4x4_t<F16>(ones4, up, l_acc[j]);
       }
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) o_acc[j][db] = mfma32x32x16(vf[db][s], pb[s], o_acc[j][db]);
+        for (int s = 0; s < 2; ++s)
+          o_acc[j][db] = mfma32x32x16_t<F16>(vf[db][s], pb[s], o_acc[j][db]);
     }
 
     wait_next();
@@ -487,10 +507,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = db * 32 + 8 * g + 4 * hi;
-          const bf16x4 ov = {(__bf16)(o_acc[j][db][4 * g + 0] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 1] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 2] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 3] * inv)};
+          const bf16x4 ov = {f32_to_half<F16>(o_acc[j][db][4 * g + 0] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 1] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 2] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 3] * inv)};
           *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
         }
       if (p.lse && hi == 0)
@@ -538,6 +558,7 @@ struct alignas(16) MainTile {
   float rec[256];
 };
 
+template <bool F16>
 __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   __shared__ MainTile ring0, ring1, ring2, ring3, ring4;
   __shared__ float rec_sink[256];
@@ -568,7 +589,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
       qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
                             : bf16x8{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)qf[j][ks][e], (float)qf[j][ks][e], ss);
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(qf[j][ks][e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
     }
     q_norm[j] = __builtin_sqrtf(sum_halves(ss));
   }
@@ -618,7 +642,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     l_acc[j] = f32x4{};
     o_acc[j][0] = f32x16{};
     o_acc[j][1] = f32x16{};
-    m_off[j] = __builtin_fmaf(q_norm[j], row_k, row_b);
+    m_off[j] = __builtin_fmaf(q_norm[j], row_k, row_b) - kShift<F16>;
   }
 
   // S(T) for both blocks; the accumulators start from the keys' bias values.
@@ -636,7 +660,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     for (int ks = 0; ks < 4; ++ks) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]);
 #pragma unroll
-      for (int j = 0; j < kBlk; ++j) sv[j] = mfma32x32x16(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
+      for (int j = 0; j < kBlk; ++j)
+        sv[j] = mfma32x32x16_t<F16>(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
     }
   };
   // V^T fragments of a tile (shared by both blocks).
@@ -655,7 +680,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
       }
   };
   // P = 2^(S c - m) of one block in bf16, its row sums, then O += V^T . P.
-  const bf16x4 ones4 = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+  const __bf16 one = f32_to_half<F16>(1.0f);
+  const bf16x4 ones4 = {one, one, one, one};
   auto softmax_pv = [&](const f32x16& sv, int j, const bf16x8 (&vf)[2][2]) {
     const float neg_m = -m_off[j];
     bf16x8 pb[2];
@@ -665,19 +691,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
       for (int e = 0; e < 8; e += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
-        const bf16x2 pv2 = {(__bf16)p0, (__bf16)p1};
+        const bf16x2 pv2 = pack2<F16>(p0, p1);
         pb[half][e] = pv2[0];
         pb[half][e + 1] = pv2[1];
       }
       const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
       const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
-      l_acc[j] = mfma4x4x4(ones4, lo, l_acc[j]);
-      l_acc[j] = mfma4x4x4(ones4, up, l_acc[j]);
+      l_acc[j] = mfma4x4x4_t<F16>(ones4, lo, l_acc[j]);
+      l_acc[j] = mfma4x4x4_t<F16>(ones4, up, l_acc[j]);
     }
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) o_acc[j][db] = mfma32x32x16(vf[db][s], pb[s], o_acc[j][db]);
+      for (int s = 0; s < 2; ++s) o_acc[j][db] = mfma32x32x16_t<F16>(vf[db][s], pb[s], o_acc[j][db]);
   };
 
   f32x16 s_cur[kBlk], s_nxt[kBlk];
@@ -702,7 +728,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
 #pragma unroll
     for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s_cur[j][r]), s_cur[j][r + 1]);
     mx = fmaxf(mx, s_cur[j][15]);
-    bad = bad || !(m_off[j] - max_halves(mx) * c <= kGap);
+    bad = bad || !(m_off[j] - max_halves(mx) * c <= kGap<F16> - kShift<F16>);
   }
   const bool fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
   wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
@@ -764,10 +790,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = db * 32 + 8 * g + 4 * hi;
-          const bf16x4 ov = {(__bf16)(o_acc[j][db][4 * g + 0] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 1] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 2] * inv),
-                             (__bf16)(o_acc[j][db][4 * g + 3] * inv)};
+          const bf16x4 ov = {f32_to_half<F16>(o_acc[j][db][4 * g + 0] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 1] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 2] * inv),
+                             f32_to_half<F16>(o_acc[j][db][4 * g + 3] * inv)};
           *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
         }
       if (p.lse && hi == 0)
@@ -798,43 +824,47 @@ extern "C" size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t
   return attn_ws_bytes(B, H, M, N);
 }
 
-extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v, const void* bias,
-                                     int bias_kind, int64_t bias_sb, int64_t bias_sh,
-                                     int64_t bias_sn, void* o, float* lse, int64_t B, int64_t H,
-                                     int64_t M, int64_t N, int64_t D, int64_t q_sb, int64_t q_sh,
-                                     int64_t q_sm, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                                     int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
-                                     int64_t o_sh, int64_t o_sm, int64_t lse_sb, int64_t lse_sh,
-                                     void* workspace, size_t workspace_bytes, float sm_scale,
-                                     void* stream) {
+namespace {
+
+// Shared by the bf16 and fp16 entry points; `fn` names the entry point in
+// error messages.
+template <bool F16>
+int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v,
+                     const void* bias, int bias_kind, int64_t bias_sb, int64_t bias_sh,
+                     int64_t bias_sn, void* o, float* lse, int64_t B, int64_t H, int64_t M,
+                     int64_t N, int64_t D, int64_t q_sb, int64_t q_sh, int64_t q_sm, int64_t k_sb,
+                     int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                     int64_t o_sb, int64_t o_sh, int64_t o_sm, int64_t lse_sb, int64_t lse_sh,
+                     void* workspace, size_t workspace_bytes, float sm_scale, void* stream) {
   gpa_clear_error();
   if (B < 0 || H < 0 || M < 0 || N < 0 || D < 0) {
-    gpa_set_error("gpa_attn_keybias_bf16: negative size");
+    gpa_set_error("%s: negative size", fn);
     return GPA_E_INVALID;
   }
   if (B == 0 || H == 0 || M == 0) return GPA_OK;
   if (N == 0) {
-    gpa_set_error("gpa_attn_keybias_bf16: empty key set (N=0)");
+    gpa_set_error("%s: empty key set (N=0)", fn);
     return GPA_E_INVALID;
   }
   if (D != kHD) {
-    gpa_set_error("gpa_attn_keybias_bf16: head_dim %lld unsupported (only 64)", (long long)D);
+    gpa_set_error("%s: head_dim %lld unsupported (only 64)", fn, (long long)D);
     return GPA_E_UNSUPPORTED;
   }
   if (!q || !k || !v || !o) {
-    gpa_set_error("gpa_attn_keybias_bf16: null tensor pointer");
+    gpa_set_error("%s: null tensor pointer", fn);
     return GPA_E_INVALID;
   }
-  if (bias_kind != GPA_BIAS_NONE && bias_kind != GPA_BIAS_F32 && bias_kind != GPA_BIAS_BF16) {
-    gpa_set_error("gpa_attn_keybias_bf16: unknown bias kind %d", bias_kind);
+  if (bias_kind != GPA_BIAS_NONE && bias_kind != GPA_BIAS_F32 && bias_kind != GPA_BIAS_BF16 &&
+      bias_kind != GPA_BIAS_F16) {
+    gpa_set_error("%s: unknown bias kind %d", fn, bias_kind);
     return GPA_E_INVALID;
   }
   if (bias_kind != GPA_BIAS_NONE && !bias) {
-    gpa_set_error("gpa_attn_keybias_bf16: bias kind %d with a null bias pointer", bias_kind);
+    gpa_set_error("%s: bias kind %d with a null bias pointer", fn, bias_kind);
     return GPA_E_INVALID;
   }
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) {
-    gpa_set_error("gpa_attn_keybias_bf16: sm_scale must be positive and finite");
+    gpa_set_error("%s: sm_scale must be positive and finite", fn);
     return GPA_E_INVALID;
   }
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) &&
@@ -843,12 +873,12 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
                        k_sh % 8 == 0 && v_sn % 8 == 0 && v_sb % 8 == 0 && v_sh % 8 == 0 &&
                        o_sm % 4 == 0 && o_sb % 4 == 0 && o_sh % 4 == 0;
   if (!aligned || q_sm < D || k_sn < D || v_sn < D || o_sm < D) {
-    gpa_set_error("gpa_attn_keybias_bf16: rows must have unit feature stride, q/k/v rows "
-                  "16-byte and o rows 8-byte aligned");
+    gpa_set_error("%s: rows must have unit feature stride, q/k/v rows "
+                  "16-byte and o rows 8-byte aligned", fn);
     return GPA_E_INVALID;
   }
   if (B * H > 65535) {
-    gpa_set_error("gpa_attn_keybias_bf16: B*H=%lld exceeds the grid limit", (long long)(B * H));
+    gpa_set_error("%s: B*H=%lld exceeds the grid limit", fn, (long long)(B * H));
     return GPA_E_UNSUPPORTED;
   }
   const int64_t gx = (M + kQPerWG - 1) / kQPerWG;
@@ -857,13 +887,13 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   const int64_t span = N + (kMainAhead + 1) * kKT;
   if (gx > 0x7fffffff || span * k_sn * 2 >= ((int64_t)1 << 31) ||
       span * v_sn * 2 >= ((int64_t)1 << 31)) {
-    gpa_set_error("gpa_attn_keybias_bf16: one head's K/V slice exceeds 2 GiB");
+    gpa_set_error("%s: one head's K/V slice exceeds 2 GiB", fn);
     return GPA_E_UNSUPPORTED;
   }
   const size_t ws_need = attn_ws_bytes(B, H, M, N);
   if (!workspace || workspace_bytes < ws_need || (uintptr_t)workspace % 16) {
-    gpa_set_error("gpa_attn_keybias_bf16: 16-byte aligned workspace of %zu bytes required, %zu "
-                  "given",
+    gpa_set_error("%s: 16-byte aligned workspace of %zu bytes required, %zu "
+                  "given", fn,
                   ws_need, workspace ? workspace_bytes : (size_t)0);
     return GPA_E_WORKSPACE;
   }
@@ -884,11 +914,11 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   ra.total_keys = B * H * ntiles * kKT;
   ra.mul = 1.0f / sm_scale;
   ra.c = c;
-  hipLaunchKernelGGL(tile_records_kernel, dim3((unsigned)((ra.total_keys + 255) / 256)), dim3(256),
-                     0, s, ra);
+  hipLaunchKernelGGL(tile_records_kernel<F16>, dim3((unsigned)((ra.total_keys + 255) / 256)),
+                     dim3(256), 0, s, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_attn_keybias_bf16: tile-record pre-pass launch failed: %s",
+    gpa_set_error("%s: tile-record pre-pass launch failed: %s", fn,
                   hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
@@ -897,7 +927,7 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
                      (const float*)workspace, bounds, ntiles);
   e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_attn_keybias_bf16: row-bound pre-pass launch failed: %s",
+    gpa_set_error("%s: row-bound pre-pass launch failed: %s", fn,
                   hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
@@ -925,12 +955,44 @@ extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v
   p.c = c;
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
-  hipLaunchKernelGGL(attn_main_kernel, grid, block, 0, s, p);
-  hipLaunchKernelGGL(attn_repair_kernel, grid, block, 0, s, p);
+  hipLaunchKernelGGL(attn_main_kernel<F16>, grid, block, 0, s, p);
+  hipLaunchKernelGGL(attn_repair_kernel<F16>, grid, block, 0, s, p);
   e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_attn_keybias_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+extern "C" int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v, const void* bias,
+                                     int bias_kind, int64_t bias_sb, int64_t bias_sh,
+                                     int64_t bias_sn, void* o, float* lse, int64_t B, int64_t H,
+                                     int64_t M, int64_t N, int64_t D, int64_t q_sb, int64_t q_sh,
+                                     int64_t q_sm, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                     int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
+                                     int64_t o_sh, int64_t o_sm, int64_t lse_sb, int64_t lse_sh,
+                                     void* workspace, size_t workspace_bytes, float sm_scale,
+                                     void* stream) {
+  return attn_keybias_run<false>("gpa_attn_keybias_bf16", q, k, v, bias, bias_kind, bias_sb,
+                                 bias_sh, bias_sn, o, lse, B, H, M, N, D, q_sb, q_sh, q_sm, k_sb,
+                                 k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sm, lse_sb, lse_sh,
+                                 workspace, workspace_bytes, sm_scale, stream);
+}
+
+extern "C" int gpa_attn_keybias_f16(const void* q, const void* k, const void* v, const void* bias,
+                                    int bias_kind, int64_t bias_sb, int64_t bias_sh,
+                                    int64_t bias_sn, void* o, float* lse, int64_t B, int64_t H,
+                                    int64_t M, int64_t N, int64_t D, int64_t q_sb, int64_t q_sh,
+                                    int64_t q_sm, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                    int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
+                                    int64_t o_sh, int64_t o_sm, int64_t lse_sb, int64_t lse_sh,
+                                    void* workspace, size_t workspace_bytes, float sm_scale,
+                                    void* stream) {
+  return attn_keybias_run<true>("gpa_attn_keybias_f16", q, k, v, bias, bias_kind, bias_sb,
+                                bias_sh, bias_sn, o, lse, B, H, M, N, D, q_sb, q_sh, q_sm, k_sb,
+                                k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sm, lse_sb, lse_sh,
+                                workspace, workspace_bytes, sm_scale, stream);
 }

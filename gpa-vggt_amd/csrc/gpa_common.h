@@ -12,6 +12,8 @@ namespace gpa {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -43,6 +45,65 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // (in all four result registers).
 __device__ __forceinline__ f32x4 mfma4x4x4(bf16x4 a, bf16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// The same three MFMA shapes on 16-bit operands of either format: the
+// operands travel as bf16x8 / bf16x4 bit patterns, and F16 selects the fp16
+// instruction (identical operand and result layouts).
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma32x32x16_t(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16x16x32_t(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma4x4x4_t(bf16x4 a, bf16x4 b, f32x4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4, a),
+                                              __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// A 16-bit element of either format to fp32, and fp32 to its bit pattern
+// (round to nearest even).
+template <bool F16>
+__device__ __forceinline__ float half_to_f32(__bf16 x) {
+  if constexpr (F16)
+    return (float)__builtin_bit_cast(_Float16, x);
+  else
+    return (float)x;
+}
+template <bool F16>
+__device__ __forceinline__ __bf16 f32_to_half(float x) {
+  if constexpr (F16)
+    return __builtin_bit_cast(__bf16, (_Float16)x);
+  else
+    return (__bf16)x;
+}
+
+// Two fp32 values to a packed pair of 16-bit values (round to nearest even),
+// one v_cvt_pk_{bf16,f16}_f32.  (Element-wise fp16 casts through bit casts
+// defeat the pairing; the vector conversion does not.)
+template <bool F16>
+__device__ __forceinline__ bf16x2 pack2(float a, float b) {
+  if constexpr (F16) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(bf16x2, __builtin_convertvector(f32x2{a, b}, f16x2));
+  } else {
+    return bf16x2{(__bf16)a, (__bf16)b};
+  }
 }
 
 // Raw buffer resource over `bytes` bytes at `base`.  Loads through it are

@@ -83,7 +83,7 @@ __device__ __forceinline__ void map_block(const SimArgs& p, int bid, int& mblock
   }
 }
 
-template <int KS>
+template <int KS, bool F16>
 __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
   constexpr int kSB = src_blocks(KS);
   constexpr int kRowsPerWG = rows_per_wg(KS);
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
         const bf16x8 af =
             *reinterpret_cast<const bf16x8*>(L + row * ROW_BYTES + ((ch ^ (row & SWZ)) << 4));
 #pragma unroll
-        for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32(af, sf[sb][ks], acc[sb]);
+        for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32_t<F16>(af, sf[sb][ks], acc[sb]);
       }
       const int tile = (int)(tile_n >> 4);
       if (tile_n + 16 <= n_end) {
@@ -276,6 +276,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
 constexpr int kPipeRing = 8;                 // 16-row tile slots
 constexpr int kPipePairsAhead = kPipeRing / 2 - 1;
 
+template <bool F16>
 __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
   constexpr int KS = 4, kSB = 4, D = 128;
   constexpr int kRowsPerWG = rows_per_wg(KS);
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
     for (int ks = 0; ks < KS; ++ks) {
       const bf16x8 af = *reinterpret_cast<const bf16x8*>(T + a_off[ks]);
 #pragma unroll
-      for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32(af, sf[sb][ks], acc[sb]);
+      for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32_t<F16>(af, sf[sb][ks], acc[sb]);
     }
   };
   // Running max / first tile reaching it, per slot (strict >: an earlier
@@ -537,45 +538,49 @@ extern "C" size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N
   return make_plan(B, M, N, D).ws_bytes;
 }
 
-extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max, int64_t* out_idx,
-                                   int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
-                                   int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
-                                   int64_t oidx_sb, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+namespace {
+
+// Shared by the bf16 and fp16 entry points: the kernels differ only in the
+// MFMA instruction; `fn` names the entry point in error messages.
+template <bool F16>
+int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max, int64_t* out_idx,
+                   int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb, int64_t a_sm,
+                   int64_t b_sb, int64_t b_sn, int64_t omax_sb, int64_t oidx_sb, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   gpa_clear_error();
   if (B < 0 || M < 0 || N < 0 || D < 0) {
-    gpa_set_error("gpa_sim_argmax_bf16: negative size (B=%lld M=%lld N=%lld D=%lld)",
+    gpa_set_error("%s: negative size (B=%lld M=%lld N=%lld D=%lld)", fn,
                   (long long)B, (long long)M, (long long)N, (long long)D);
     return GPA_E_INVALID;
   }
   if (B == 0 || M == 0) return GPA_OK;
   if (N == 0) {
-    gpa_set_error("gpa_sim_argmax_bf16: empty destination set (N=0)");
+    gpa_set_error("%s: empty destination set (N=0)", fn);
     return GPA_E_INVALID;
   }
   if (!a || !b || !out_max || !out_idx) {
-    gpa_set_error("gpa_sim_argmax_bf16: null tensor pointer");
+    gpa_set_error("%s: null tensor pointer", fn);
     return GPA_E_INVALID;
   }
   if (D % 32 != 0 || D < 32 || D > 256) {
-    gpa_set_error("gpa_sim_argmax_bf16: feature dim D=%lld unsupported (multiple of 32, 32..256)",
+    gpa_set_error("%s: feature dim D=%lld unsupported (multiple of 32, 32..256)", fn,
                   (long long)D);
     return GPA_E_UNSUPPORTED;
   }
   if (N > (int64_t)0x7fffff00 || M > ((int64_t)1 << 40)) {
-    gpa_set_error("gpa_sim_argmax_bf16: N=%lld exceeds the int32 index range", (long long)N);
+    gpa_set_error("%s: N=%lld exceeds the int32 index range", fn, (long long)N);
     return GPA_E_UNSUPPORTED;
   }
   const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
   if ((pa % 16) || (pb % 16) || (a_sm % 8) || (b_sn % 8) || (a_sb % 8) || (b_sb % 8) ||
       a_sm < D || b_sn < D) {
-    gpa_set_error("gpa_sim_argmax_bf16: rows must be 16-byte aligned with unit feature stride "
-                  "(a_sm=%lld b_sn=%lld a_sb=%lld b_sb=%lld)",
+    gpa_set_error("%s: rows must be 16-byte aligned with unit feature stride "
+                  "(a_sm=%lld b_sn=%lld a_sb=%lld b_sb=%lld)", fn,
                   (long long)a_sm, (long long)b_sn, (long long)a_sb, (long long)b_sb);
     return GPA_E_INVALID;
   }
   if (B > 65535) {
-    gpa_set_error("gpa_sim_argmax_bf16: batch %lld exceeds the grid limit", (long long)B);
+    gpa_set_error("%s: batch %lld exceeds the grid limit", fn, (long long)B);
     return GPA_E_UNSUPPORTED;
   }
 
@@ -584,7 +589,7 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   // tiles fetched past its end (two stages, or eight 16-row tiles), must
   // stay below 2^31 bytes.
   if ((pl.n_chunk + 2 * kTN) * b_sn * 2 >= ((int64_t)1 << 31)) {
-    gpa_set_error("gpa_sim_argmax_bf16: destination split exceeds 2 GiB (N=%lld, row stride %lld)",
+    gpa_set_error("%s: destination split exceeds 2 GiB (N=%lld, row stride %lld)", fn,
                   (long long)N, (long long)b_sn);
     return GPA_E_UNSUPPORTED;
   }
@@ -606,7 +611,7 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   p.n_chunk = pl.n_chunk;
   if (pl.splits > 1) {
     if (!workspace || workspace_bytes < pl.ws_bytes) {
-      gpa_set_error("gpa_sim_argmax_bf16: workspace of %zu bytes required, %zu given",
+      gpa_set_error("%s: workspace of %zu bytes required, %zu given", fn,
                     pl.ws_bytes, workspace ? workspace_bytes : (size_t)0);
       return GPA_E_WORKSPACE;
     }
@@ -615,20 +620,20 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
   }
   const int64_t grid_x = (int64_t)pl.mblocks * pl.splits;
   if (grid_x > 0x7fffffff) {
-    gpa_set_error("gpa_sim_argmax_bf16: grid too large");
+    gpa_set_error("%s: grid too large", fn);
     return GPA_E_UNSUPPORTED;
   }
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)grid_x, (unsigned)B), block(256);
   switch (D / 32) {
 #define GPA_SIM_CASE(ks) \
-  case ks: hipLaunchKernelGGL(sim_argmax_kernel<ks>, grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL(sim_argmax_d128_kernel, grid, block, 0, s, p); break;
+  case ks: hipLaunchKernelGGL((sim_argmax_kernel<ks, F16>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL(sim_argmax_d128_kernel<F16>, grid, block, 0, s, p); break;
     GPA_SIM_CASE(1) GPA_SIM_CASE(2) GPA_SIM_CASE(3)
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      gpa_set_error("gpa_sim_argmax_bf16: D=%lld has no kernel instance", (long long)D);
+      gpa_set_error("%s: D=%lld has no kernel instance", fn, (long long)D);
       return GPA_E_UNSUPPORTED;
   }
   hipError_t e = hipGetLastError();
@@ -639,8 +644,30 @@ extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max,
     e = hipGetLastError();
   }
   if (e != hipSuccess) {
-    gpa_set_error("gpa_sim_argmax_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max, int64_t* out_idx,
+                                   int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
+                                   int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
+                                   int64_t oidx_sb, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return sim_argmax_run<false>("gpa_sim_argmax_bf16", a, b, out_max, out_idx, B, M, N, D, a_sb,
+                               a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace, workspace_bytes,
+                               stream);
+}
+
+extern "C" int gpa_sim_argmax_f16(const void* a, const void* b, float* out_max, int64_t* out_idx,
+                                  int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
+                                  int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
+                                  int64_t oidx_sb, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  return sim_argmax_run<true>("gpa_sim_argmax_f16", a, b, out_max, out_idx, B, M, N, D, a_sb,
+                              a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace, workspace_bytes,
+                              stream);
 }

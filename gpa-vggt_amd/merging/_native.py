@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -44,6 +44,7 @@ GPA_E_LAUNCH = -4
 GPA_BIAS_NONE = 0
 GPA_BIAS_F32 = 1
 GPA_BIAS_BF16 = 2
+GPA_BIAS_F16 = 3
 
 GPA_DTYPE_F32 = 0
 GPA_DTYPE_BF16 = 1
@@ -77,6 +78,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _i64, _i64,                    # omax_sb, oidx_sb
         _vp, ctypes.c_size_t, _vp,     # workspace, workspace_bytes, stream
     ]
+    lib.gpa_sim_argmax_f16.restype = ctypes.c_int
+    lib.gpa_sim_argmax_f16.argtypes = lib.gpa_sim_argmax_bf16.argtypes
     lib.gpa_attn_keybias_workspace_bytes.restype = ctypes.c_size_t
     lib.gpa_attn_keybias_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.gpa_attn_keybias_bf16.restype = ctypes.c_int
@@ -94,6 +97,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_size_t,          # workspace, workspace_bytes
         ctypes.c_float, _vp,           # sm_scale, stream
     ]
+    lib.gpa_attn_keybias_f16.restype = ctypes.c_int
+    lib.gpa_attn_keybias_f16.argtypes = lib.gpa_attn_keybias_bf16.argtypes
     lib.gpa_lse_combine_bf16.restype = ctypes.c_int
     lib.gpa_lse_combine_bf16.argtypes = [_vp] * 5 + [_i64] * 5 + [_i64] * 16 + [_i64] * 3 + [_vp]
     lib.gpa_qk_norm_rope_bf16.restype = ctypes.c_int
@@ -155,7 +160,8 @@ def exported_symbols() -> Tuple[str, ...]:
     return ("gpa_abi_version", "gpa_last_error", "gpa_sim_argmax_workspace_bytes",
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
-            "gpa_pool_shared_bf16", "gpa_merge_metric_bf16")
+            "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
+            "gpa_attn_keybias_f16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -209,10 +215,12 @@ def _rows_ok(t: torch.Tensor, align_elems: int) -> bool:
 
 @torch.library.custom_op("gpa::sim_argmax", mutates_args=())
 def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Row max (fp32) and lowest-index argmax (int64) of a @ b^T, bf16 inputs."""
+    """Row max (fp32) and lowest-index argmax (int64) of a @ b^T; a and b
+    both bf16 or both fp16."""
     dev = _require_gpu(a, b)
-    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
-        raise ValueError(f"gpa::sim_argmax takes bf16 inputs, got {a.dtype}/{b.dtype}")
+    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"gpa::sim_argmax takes two bf16 or two fp16 inputs, got "
+                         f"{a.dtype}/{b.dtype}")
     if a.dim() != 3 or b.dim() != 3 or a.shape[0] != b.shape[0] or a.shape[2] != b.shape[2]:
         raise ValueError(f"gpa::sim_argmax shape mismatch: a {tuple(a.shape)}, b {tuple(b.shape)}")
     if not _rows_ok(a, 8):
@@ -229,7 +237,8 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Te
     ws_bytes = L.gpa_sim_argmax_workspace_bytes(B, M, N, D)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(dev):
-        rc = L.gpa_sim_argmax_bf16(
+        fn = L.gpa_sim_argmax_f16 if a.dtype == torch.float16 else L.gpa_sim_argmax_bf16
+        rc = fn(
             a.data_ptr(), b.data_ptr(), out_max.data_ptr(), out_idx.data_ptr(),
             B, M, N, D, _st(a, 0), _rs(a, 1), _st(b, 0), _rs(b, 1),
             _st(out_max, 0), _st(out_idx, 0),
@@ -252,17 +261,20 @@ def _sim_argmax_fake(a, b):
 def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  bias: Optional[torch.Tensor], sm_scale: float,
                  return_lse: bool) -> Tuple[torch.Tensor, torch.Tensor]:
-    """softmax(q k^T * sm_scale + bias) v with bf16 q/k/v and a per-key bias.
+    """softmax(q k^T * sm_scale + bias) v with a per-key bias.
 
-    q [B,H,M,64], k/v [B,H,N,64] bf16; bias broadcastable to [B,H,1,N]
-    (fp32 or bf16) or None.  Returns o [B,H,M,64] bf16 and, if return_lse,
-    the log2 log-sum-exp [B,H,M] fp32 (else an empty tensor).
+    q [B,H,M,64], k/v [B,H,N,64], all bf16 or all fp16; bias broadcastable
+    to [B,H,1,N] (fp32, bf16 or fp16) or None.  Returns o [B,H,M,64] in q's
+    dtype and, if return_lse, the log2 log-sum-exp [B,H,M] fp32 (else an
+    empty tensor).
     """
     tensors = [q, k, v] + ([bias] if bias is not None else [])
     dev = _require_gpu(*tensors)
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"gpa::attn_keybias takes bf16 or fp16 q, got {q.dtype}")
     for name, t in (("q", q), ("k", k), ("v", v)):
-        if t.dtype != torch.bfloat16:
-            raise ValueError(f"gpa::attn_keybias takes bf16 {name}, got {t.dtype}")
+        if t.dtype != q.dtype:
+            raise ValueError(f"gpa::attn_keybias: {name} is {t.dtype}, q is {q.dtype}")
         if t.dim() != 4:
             raise ValueError(f"gpa::attn_keybias: {name} must be [B,H,T,D], got {tuple(t.shape)}")
     B, H, M, D = q.shape
@@ -278,17 +290,18 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         v = v.contiguous()
     bias_kind, bias_ptr, bsb, bsh, bsn = GPA_BIAS_NONE, None, 0, 0, 0
     if bias is not None:
-        if bias.dtype not in (torch.float32, torch.bfloat16):
+        if bias.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             bias = bias.float()
         try:
             bx = bias.expand(B, H, 1, N)
         except RuntimeError as exc:
             raise ValueError(f"gpa::attn_keybias: bias {tuple(bias.shape)} does not broadcast to "
                              f"[B,H,1,N]=[{B},{H},1,{N}]") from exc
-        bias_kind = GPA_BIAS_F32 if bx.dtype == torch.float32 else GPA_BIAS_BF16
+        bias_kind = {torch.float32: GPA_BIAS_F32, torch.bfloat16: GPA_BIAS_BF16,
+                     torch.float16: GPA_BIAS_F16}[bx.dtype]
         bias_ptr = bx.data_ptr()
         bsb, bsh, bsn = _st(bx, 0), _st(bx, 1), _st(bx, 3)
-    o = torch.empty(B, H, M, D, device=dev, dtype=torch.bfloat16)
+    o = torch.empty(B, H, M, D, device=dev, dtype=q.dtype)
     lse = (torch.empty(B, H, M, device=dev, dtype=torch.float32) if return_lse
            else torch.empty(0, device=dev, dtype=torch.float32))
     if B == 0 or H == 0 or M == 0:
@@ -297,7 +310,8 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ws_bytes = L.gpa_attn_keybias_workspace_bytes(B, H, M, N)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
-        rc = L.gpa_attn_keybias_bf16(
+        fn = L.gpa_attn_keybias_f16 if q.dtype == torch.float16 else L.gpa_attn_keybias_bf16
+        rc = fn(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), bias_ptr, bias_kind, bsb, bsh, bsn,
             o.data_ptr(), lse.data_ptr() if return_lse else None,
             B, H, M, N, D,
@@ -314,7 +328,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 @attn_keybias.register_fake
 def _attn_keybias_fake(q, k, v, bias, sm_scale, return_lse):
     B, H, M, D = q.shape
-    o = q.new_empty(B, H, M, D, dtype=torch.bfloat16)
+    o = q.new_empty(B, H, M, D)
     lse = q.new_empty((B, H, M) if return_lse else (0,), dtype=torch.float32)
     return o, lse
 

@@ -7,10 +7,10 @@ hand-written HIP kernel `attn_keybias_kernel` in `csrc/attn_keybias.hip`,
 reached through the `gpa::attn_keybias` custom op.
 
 Math matches SDPA(q, k, v, attn_mask=bias): scores = q@k^T * scale + bias,
-softmax over keys in fp32, P rounded to bf16 for the P@V product, fp32
-accumulation.  With return_lse the log2 softmax denominators come back as
-well, so callers can split the key set and recombine exactly
-(reference :123-127); `combine_by_lse` is that recombination for the
+softmax over keys in fp32, P rounded to the operand format (bf16 or fp16)
+for the P@V product, fp32 accumulation.  With return_lse the log2 softmax
+denominators come back as well, so callers can split the key set and
+recombine exactly (reference :123-127); `combine_by_lse` is that recombination for the
 frame-special split path of vggt/layers/attention.py:148-176.
 """
 from __future__ import annotations
@@ -34,18 +34,19 @@ def attention_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       bias: torch.Tensor, sm_scale: float, return_lse: bool = False):
     """SDPA(q, k, v, attn_mask=bias) where bias is per-key: [B, H, 1, N].
 
-    q [B, H, M, D], k/v [B, H, N, D] (GPU, bf16; fp32 inputs are cast to the
-    autocast dtype or bf16 first, as at merging/fused_attention.py:139-144).
-    Returns [B, H, M, D]; with return_lse also [B, H, M] fp32 log2 softmax
-    denominators.  `bias` may be None (plain attention).
+    q [B, H, M, D], k/v [B, H, N, D] (GPU, bf16 or fp16; fp32 inputs are cast
+    to the autocast dtype or bf16 first, as at merging/fused_attention.py:
+    139-144).  Returns [B, H, M, D] in q's dtype; with return_lse also
+    [B, H, M] fp32 log2 softmax denominators.  `bias` may be None (plain
+    attention).
     """
     if q.dtype == torch.float32:
         dt = _autocast_dtype()
         q, k, v = q.to(dt), k.to(dt), v.to(dt)
         bias = None if bias is None else bias.to(dt)
-    if q.dtype != torch.bfloat16:
+    if q.dtype not in (torch.bfloat16, torch.float16):
         raise NotImplementedError(
-            f"attention_keybias: {q.dtype} is not supported; the gfx950 kernel runs bf16")
+            f"attention_keybias: {q.dtype} is not supported; the gfx950 kernels run bf16 and fp16")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("attention_keybias expects [B, H, T, D] q/k/v")
     v = v.to(q.dtype)

@@ -6,7 +6,7 @@ name, arguments, dtype contract and return types
 hand-written HIP kernel `sim_argmax_kernel` in `csrc/sim_argmax.hip`,
 reached through the `gpa::sim_argmax` custom op.
 
-Numerics: fp32 accumulation of bf16 products; the max is taken over the fp32
+Numerics: fp32 accumulation of bf16 (or fp16) products; the max is taken over the fp32
 scores (not bf16-rounded scores as in the chunked torch path), and ties
 resolve to the lowest destination index, as the reference kernel's strict
 `>` across tiles plus `tl.argmax`'s first index do
@@ -27,23 +27,23 @@ _MAX_D = 256
 def fused_similarity_argmax(a: torch.Tensor, b: torch.Tensor):
     """node_max, node_idx = (a @ b.transpose(-1,-2)).max(dim=-1), fused.
 
-    a: [B, M, D] src metric, b: [B, N, D] dst metric (GPU, bf16 or fp32).
-    Returns node_max [B, M] (a.dtype) and node_idx [B, M] (int64).
-    Follows merging/fused_similarity.py:81-112: fp32 inputs are rounded to
-    bf16 first (:90-95), the max comes back in the input dtype (:112).
+    a: [B, M, D] src metric, b: [B, N, D] dst metric (GPU, fp16, bf16 or
+    fp32).  Returns node_max [B, M] (a.dtype) and node_idx [B, M] (int64).
+    Follows merging/fused_similarity.py:81-112: an fp32 `a` rounds both
+    operands to bf16 first (:90-95); fp16 operands run the fp16 MFMA; the max
+    comes back in a's dtype (:112).
     """
     if not (a.is_cuda and b.is_cuda and a.dim() == 3 and b.dim() == 3):
         raise AssertionError(
             "fused_similarity_argmax expects 3-D GPU tensors "
             f"(got a {tuple(a.shape)} on {a.device}, b {tuple(b.shape)} on {b.device})")
     out_dtype = a.dtype
-    if a.dtype == torch.float16 or b.dtype == torch.float16:
-        raise NotImplementedError("fused_similarity_argmax: fp16 inputs are not supported; "
-                                  "the gfx950 kernel runs bf16 (pass bf16 or fp32)")
     if a.dtype == torch.float32:
         a = a.to(torch.bfloat16)
-    if b.dtype == torch.float32:
         b = b.to(torch.bfloat16)
+    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"fused_similarity_argmax: a is {a.dtype}, b is {b.dtype}; the kernel "
+                         "takes two bf16 or two fp16 operands (fp32 a casts both to bf16)")
     D = a.shape[-1]
     if b.shape[-1] != D:
         raise ValueError(f"feature dims differ: {D} vs {b.shape[-1]}")

@@ -1,7 +1,8 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Seven entry points (and their kernels) sit behind this boundary:
+ * Seven entry points (two of them with an fp16 twin) sit behind this
+ * boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -45,7 +46,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 6
+#define GPA_ABI_VERSION 7
 
 enum {
   GPA_OK = 0,
@@ -55,8 +56,8 @@ enum {
   GPA_E_LAUNCH = -4        /* the HIP runtime rejected the launch */
 };
 
-/* Bias element types accepted by gpa_attn_keybias_bf16. */
-enum { GPA_BIAS_NONE = 0, GPA_BIAS_F32 = 1, GPA_BIAS_BF16 = 2 };
+/* Bias element types accepted by gpa_attn_keybias_bf16 / _f16. */
+enum { GPA_BIAS_NONE = 0, GPA_BIAS_F32 = 1, GPA_BIAS_BF16 = 2, GPA_BIAS_F16 = 3 };
 
 /* Element types and reductions of gpa_merge_heads. */
 enum { GPA_DTYPE_F32 = 0, GPA_DTYPE_BF16 = 1, GPA_DTYPE_F16 = 2 };
@@ -92,6 +93,19 @@ int gpa_sim_argmax_bf16(const void* a, const void* b,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* The same on fp16 a and b (v_mfma_f32_16x16x32_f16; same arguments, same
+ * workspace).  Replaces fused_similarity.py:81-112 for fp16 operands, which
+ * the reference passes to its kernel as they are (only an fp32 `a` is cast,
+ * to bf16). */
+int gpa_sim_argmax_f16(const void* a, const void* b,
+                       float* out_max, int64_t* out_idx,
+                       int64_t B, int64_t M, int64_t N, int64_t D,
+                       int64_t a_sb, int64_t a_sm,
+                       int64_t b_sb, int64_t b_sn,
+                       int64_t omax_sb, int64_t oidx_sb,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /* Bytes of device workspace gpa_attn_keybias_bf16 needs: per (batch, head)
  * one 144-byte record per 32-key tile, holding the keys' bias/sm_scale
  * (padded past N) and two per-tile maxima the kernel bounds its scores with,
@@ -125,6 +139,25 @@ int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
                           int64_t lse_sb, int64_t lse_sh,
                           void* workspace, size_t workspace_bytes,
                           float sm_scale, void* stream);
+
+/* The same on fp16 q, k, v and o (fp16 MFMA; P rounded to fp16 for P.V,
+ * fp32 softmax and accumulation; same arguments and workspace).  The fixed
+ * offset of the main pass sits 15 below the score bound, so P <= 2^15 fits
+ * fp16, and is certified only where every row max is within 16 of the
+ * bound (else the repair pass rescales lazily at 2^15).  Replaces
+ * fused_attention.py:130-180 under fp16 autocast (its :139-144 cast). */
+int gpa_attn_keybias_f16(const void* q, const void* k, const void* v,
+                         const void* bias, int bias_kind,
+                         int64_t bias_sb, int64_t bias_sh, int64_t bias_sn,
+                         void* o, float* lse,
+                         int64_t B, int64_t H, int64_t M, int64_t N, int64_t D,
+                         int64_t q_sb, int64_t q_sh, int64_t q_sm,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                         int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                         int64_t o_sb, int64_t o_sh, int64_t o_sm,
+                         int64_t lse_sb, int64_t lse_sh,
+                         void* workspace, size_t workspace_bytes,
+                         float sm_scale, void* stream);
 
 /*
  * Deterministic segmented reduction of token rows: the K/V merge.
