@@ -165,16 +165,22 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Tile records: one thread per key; the 32 lanes of a tile reduce the two
-// maxima with cross-lane shuffles.  Keys past N get bias -inf and |k| = 0.
+// Tile records: one workgroup per 32-key tile, eight lanes per key row (one
+// 16-byte chunk each), so a wave's loads cover eight whole 128-byte rows
+// and the rows stream at HBM rate.  The lanes of a key reduce its |k|^2;
+// the tile's two maxima meet across the wave (xor 8, 16, 32) and then the
+// four waves in LDS.  Keys past N get bias -inf and |k| = 0.
 template <bool F16>
 __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over B*H*ntiles*32
-  const bool live = i < a.total_keys;
-  const int64_t n = i % (a.ntiles * kKT), row = i / (a.ntiles * kKT);
+  __shared__ float part[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t tile = blockIdx.x;                     // over B*H*ntiles
+  const int64_t row = tile / a.ntiles, t = tile % a.ntiles;
   const int64_t hb = row % a.H, bb = row / a.H;
-  float x = -INFINITY, kn = 0.f;
-  if (live && n < a.N) {
+  const int j = tid >> 3, ch = tid & 7;                // key of the tile, 16-byte chunk
+  const int64_t n = t * kKT + j;
+  float x = -INFINITY, ss = 0.f;
+  if (n < a.N) {
     const int64_t off = bb * a.sb + hb * a.sh + n * a.sn;
     if (a.kind == GPA_BIAS_F32)
       x = static_cast<const float*>(a.bias)[off] * a.mul;
@@ -184,30 +190,34 @@ __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
       x = (float)static_cast<const _Float16*>(a.bias)[off] * a.mul;
     else
       x = 0.f;
-    const bf16x8* kr = reinterpret_cast<const bf16x8*>(a.k + bb * a.k_sb + hb * a.k_sh + n * a.k_sn);
-    float ss = 0.f;
+    const bf16x8 v =
+        *reinterpret_cast<const bf16x8*>(a.k + bb * a.k_sb + hb * a.k_sh + n * a.k_sn + ch * 8);
 #pragma unroll
-    for (int j = 0; j < kHD / 8; ++j) {
-      const bf16x8 v = kr[j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = half_to_f32<F16>(v[e]);
-        ss = __builtin_fmaf(f, f, ss);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const float f = half_to_f32<F16>(v[e]);
+      ss = __builtin_fmaf(f, f, ss);
     }
-    kn = __builtin_sqrtf(ss);
   }
-  float kmax = kn, xmax = x;
 #pragma unroll
-  for (int w = 1; w < kKT; w <<= 1) {
-    kmax = fmaxf(kmax, __shfl_xor(kmax, w, kKT));
-    xmax = fmaxf(xmax, __shfl_xor(xmax, w, kKT));
+  for (int w = 1; w < 8; w <<= 1) ss += __shfl_xor(ss, w);
+  float kmax = __builtin_sqrtf(ss), xmax = x;
+#pragma unroll
+  for (int w = 8; w < 64; w <<= 1) {
+    kmax = fmaxf(kmax, __shfl_xor(kmax, w));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, w));
   }
-  if (!live) return;
-  float* rec = a.recs + (row * a.ntiles + n / kKT) * kRec;
-  const int j = (int)(n % kKT);
-  rec[j] = x;
-  if (j < kRec - kKT) rec[kKT + j] = j == 0 ? a.c * kmax : j == 1 ? a.c * xmax : 0.f;
+  if (lane == 0) {
+    part[0][wave] = kmax;
+    part[1][wave] = xmax;
+  }
+  float* rec = a.recs + tile * kRec;
+  if (ch == 0) rec[j] = x;
+  __syncthreads();
+  if (tid < kRec - kKT) {
+    const float km = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
+    const float xm = fmaxf(fmaxf(part[1][0], part[1][1]), fmaxf(part[1][2], part[1][3]));
+    rec[kKT + tid] = tid == 0 ? a.c * km : tid == 1 ? a.c * xm : 0.f;
+  }
 }
 
 // Per (batch, head): the maxima over its tiles of c*max|k| and
@@ -912,10 +922,14 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   ra.N = N;
   ra.ntiles = ntiles;
   ra.total_keys = B * H * ntiles * kKT;
+  if (B * H * ntiles > 0x7fffffff) {
+    gpa_set_error("%s: %lld key tiles exceed the grid limit", fn, (long long)(B * H * ntiles));
+    return GPA_E_UNSUPPORTED;
+  }
   ra.mul = 1.0f / sm_scale;
   ra.c = c;
-  hipLaunchKernelGGL(tile_records_kernel<F16>, dim3((unsigned)((ra.total_keys + 255) / 256)),
-                     dim3(256), 0, s, ra);
+  hipLaunchKernelGGL(tile_records_kernel<F16>, dim3((unsigned)(B * H * ntiles)), dim3(256), 0, s,
+                     ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("%s: tile-record pre-pass launch failed: %s", fn,

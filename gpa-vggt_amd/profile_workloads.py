@@ -1,11 +1,15 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|attn|merge|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|attn|merge|front|pool|sim16|attn16|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   attn   biased attention, 16 heads x 274,800 queries x 68,700 keys x 64
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
+  front  merge front end: 274,800 fp32 metric rows of 1024 -> bf16 [dst | src] x 128
+  pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
+  sim16  the similarity workload in fp16
+  attn16 the attention workload in fp16
   copy   a plain device copy of 1 GiB (bf16), the calibration for HBM byte
          counters: FETCH_SIZE / WRITE_SIZE of this dispatch should read
          1 GiB each, and the ratio to that is the counters' scale factor
@@ -30,7 +34,7 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "attn", "merge", "copy", "all"):
+    if which not in ("sim", "attn", "merge", "front", "pool", "sim16", "attn16", "copy", "all"):
         print(__doc__, file=sys.stderr)
         return 2
 
@@ -63,12 +67,47 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"merge [1,16,274800,64] f32 -> 66845 slots x {reps} done", flush=True)
         del t, off, tok
-    if which in ("attn", "all"):
-        q, k, v, b = W.attn_inputs(device=dev)
+    if which in ("front", "all"):
+        from merging.merge import _projection, dst_mask
+        g = torch.Generator(device=dev)
+        g.manual_seed(33)
+        order = torch.argsort(dst_mask(200, 37, 37, 2, 2, 5, False, g, dev), stable=True)
+        metric = torch.randn(1, 200 * 1374, 1024, device=dev)
+        proj = _projection(dev, 1024, 128)
         for _ in range(reps):
-            attention_keybias(q, k, v, b, 0.125)
+            _native.merge_metric(metric, proj, order, False)
         torch.cuda.synchronize()
-        print(f"attn 16x274800x68700x64 x {reps} done", flush=True)
+        print(f"front 274800x1024 f32 -> 128 x {reps} done", flush=True)
+        del metric, order
+    if which in ("pool", "all"):
+        kk = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        vv = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        for _ in range(reps):
+            torch.ops.gpa.pool_shared(kk, vv, 200, 5, 37, 8, False)
+        torch.cuda.synchronize()
+        print(f"pool 16x200 frames kp 8 x {reps} done", flush=True)
+        del kk, vv
+    if which in ("sim16", "all"):
+        s, d = W.sim_inputs(device=dev)
+        s, d = s.half(), d.half()
+        for _ in range(reps):
+            fused_similarity_argmax(s, d)
+        torch.cuda.synchronize()
+        print(f"sim16 75000x25000x128 x {reps} done", flush=True)
+        del s, d
+    if which in ("attn", "attn16", "all"):
+        q, k, v, b = W.attn_inputs(device=dev)
+        if which in ("attn", "all"):
+            for _ in range(reps):
+                attention_keybias(q, k, v, b, 0.125)
+            torch.cuda.synchronize()
+            print(f"attn 16x274800x68700x64 x {reps} done", flush=True)
+        if which in ("attn16", "all"):
+            q, k, v, b = q.half(), k.half(), v.half(), b.half()
+            for _ in range(reps):
+                attention_keybias(q, k, v, b, 0.125)
+            torch.cuda.synchronize()
+            print(f"attn16 16x274800x68700x64 x {reps} done", flush=True)
     return 0
 
 
