@@ -4,8 +4,10 @@
 //   lse[m]  = log2 sum_n 2^((q_m.k_n * sm_scale + bias_n) * log2 e)
 //
 // Semantics follow merging/fused_attention.py:70-127: scores in the exp2
-// domain, fp32 online softmax, P rounded to bf16 for the P.V product, fp32
-// accumulation, log2 log-sum-exp output.  Like the reference wrapper
+// domain, fp32 online softmax, P rounded to the operand format for the P.V
+// product, fp32 accumulation, log2 log-sum-exp output.  Every kernel is
+// instantiated for bf16 and for fp16 operands (F16); only the MFMA opcode,
+// the conversions and the offset constants differ.  Like the reference wrapper
 // (fused_attention.py:159-160), a small pre-pass first writes the bias to a
 // padded per-key buffer; here each 32-key tile gets a 144-byte record: the
 // 32 values bias/sm_scale (-inf past N) and the tile's score bound below.
@@ -40,8 +42,9 @@
 //     c0+i of keys base..base+3.  O^T keeps one query per lane, so a
 //     rescale is a per-lane multiply.
 //   * The softmax offset m only has to keep 2^(x-m) in range, since P is
-//     stored in bf16, which has fp32's exponent range: m moves lazily, only
-//     when a tile could produce x > m + kTau.  Whether it could is decided
+//     stored in bf16, which has fp32's exponent range (fp16 P stops at 65504,
+//     hence kTau = 15 there): m moves lazily, only when a tile could produce
+//     x > m + kTau.  Whether it could is decided
 //     from a Cauchy-Schwarz bound, x <= c*(|q| max|k| + max bias/sm_scale)
 //     over the tile's keys (the record carries both maxima), one FMA per
 //     lane; only when the bound exceeds m + kTau does the wave take the exact
@@ -121,7 +124,7 @@ struct RecArgs {
   int H;
   int64_t k_sb, k_sh, k_sn;
   int64_t sb, sh, sn;  // bias strides (0 = broadcast)
-  int64_t N, ntiles, total_keys;
+  int64_t N, ntiles;
   float mul;  // 1 / sm_scale
   float c;    // sm_scale * log2(e)
 };
@@ -921,7 +924,6 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   ra.sb = bias_sb; ra.sh = bias_sh; ra.sn = bias_sn;
   ra.N = N;
   ra.ntiles = ntiles;
-  ra.total_keys = B * H * ntiles * kKT;
   if (B * H * ntiles > 0x7fffffff) {
     gpa_set_error("%s: %lld key tiles exceed the grid limit", fn, (long long)(B * H * ntiles));
     return GPA_E_UNSUPPORTED;

@@ -2,7 +2,7 @@
 //
 // Computes, for every source row m of a[B, M, D] against every destination
 // row n of b[B, N, D]:
-//     out_max[m] = max_n <a_m, b_n>        (bf16 inputs, fp32 accumulate)
+//     out_max[m] = max_n <a_m, b_n>        (bf16 or fp16 inputs, fp32 accumulate)
 //     out_idx[m] = lowest n attaining it
 // without materialising the M x N score matrix.  Semantics follow the
 // reference Triton kernel merging/fused_similarity.py:33-78 (fp32 scores,
@@ -14,7 +14,7 @@
 //     rows stay in VGPRs as MFMA B-operands for the whole kernel; destination
 //     rows stream through LDS in double-buffered stages of 64 rows.
 //   * Each 16x16 score tile is S^T = Dst(16xD) . Src^T(Dx16) on
-//     v_mfma_f32_16x16x32_bf16, so a lane holds one source row against 4
+//     v_mfma_f32_16x16x32_bf16 (_f16 in the fp16 instantiation), so a lane holds one source row against 4
 //     destination rows and the running max/argmax is lane-local: one
 //     compare and two selects per score, no cross-lane traffic until the
 //     very end.  (The 16x16 shape keeps 16 tracking slots per source row,
