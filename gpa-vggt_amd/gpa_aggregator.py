@@ -82,6 +82,7 @@ class GpaConfig:
     merge_metric_dim: int = 128
     merge_grid: int = 2
     frame_attn: str = "gpa"            # "gpa" (attention kernel, bias=None) or "sdpa"
+    fused_norms: bool = True           # residual + LayerScale + LayerNorm kernel (bf16 blocks)
     vit_depth: int = 24                # DINOv2 ViT-L/14 blocks
     dpt_blocks: Tuple[int, ...] = (4, 11, 17, 23)   # outputs kept (aggregator.py:296)
 
@@ -347,7 +348,27 @@ class Block(nn.Module):
         self.mlp = Mlp(dim, int(dim * mlp_ratio))
         self.ls2 = LayerScale(dim, ls_init)
 
+    def _fused_ok(self, x: torch.Tensor) -> bool:
+        """The fused kernel reproduces the bf16 chain: a bf16 block on a bf16
+        stream, under bf16 autocast or none."""
+        if not (self.attn.cfg.fused_norms and x.is_cuda and x.dtype == torch.bfloat16
+                and x.shape[-1] % 512 == 0 and self.norm1.weight.dtype == torch.bfloat16
+                and self.ls1.gamma.dtype == torch.bfloat16):
+            return False
+        return (not torch.is_autocast_enabled("cuda")
+                or torch.get_autocast_dtype("cuda") == torch.bfloat16)
+
     def forward(self, x, rope: Optional[RopeTable] = None, global_merging=None):
+        if self._fused_ok(x):
+            # block.py:84-96 with the elementwise steps fused: LayerNorm 1 to
+            # bf16; x + ls1(attn) with LayerNorm 2 in one pass; x + ls2(mlp).
+            rl = torch.ops.gpa.residual_layernorm
+            _, ln1 = rl(x, None, None, self.norm1.weight, self.norm1.bias, self.norm1.eps, False)
+            a = self.attn(ln1, rope, global_merging)
+            h, ln2 = rl(x, a, self.ls1.gamma, self.norm2.weight, self.norm2.bias,
+                        self.norm2.eps, True)
+            out, _ = rl(h, self.mlp(ln2), self.ls2.gamma, None, None, 0.0, True)
+            return out
         x = x + self.ls1(self.attn(self.norm1(x), rope, global_merging))
         return x + self.ls2(self.mlp(self.norm2(x)))
 

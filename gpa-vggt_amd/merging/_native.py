@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -124,6 +124,13 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, _i64, _vp, ctypes.c_int,  # proj, P, order, norm_mode
         _vp, _vp,                      # out, stream
     ]
+    lib.gpa_residual_layernorm_bf16.restype = ctypes.c_int
+    lib.gpa_residual_layernorm_bf16.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, ctypes.c_float,  # x, y, gamma, weight, bias, eps
+        _i64, _i64, _i64, _i64,        # rows, C, x_sn, y_sn
+        _vp, _i64, _vp, _i64,          # h_out, h_sn, ln_out, ln_sn
+        _vp,                           # stream
+    ]
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -161,7 +168,7 @@ def exported_symbols() -> Tuple[str, ...]:
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
             "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
-            "gpa_attn_keybias_f16")
+            "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -596,3 +603,61 @@ def merge_metric(metric: torch.Tensor, proj: torch.Tensor, order: Optional[torch
 def _merge_metric_fake(metric, proj, order, norm_bf16):
     B, N, _ = metric.shape
     return metric.new_empty(B, N, proj.shape[1], dtype=torch.bfloat16)
+
+
+# --------------------------------------------------------------------------
+# gpa::residual_layernorm
+# --------------------------------------------------------------------------
+
+@torch.library.custom_op("gpa::residual_layernorm", mutates_args=())
+def residual_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], gamma: Optional[torch.Tensor],
+                       weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float,
+                       want_h: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """h = bf16(x + bf16(gamma * y)) (h = x without y) and LayerNorm(h) in
+    bf16, over the last dim of bf16 x / y.  Returns (h if want_h else an
+    empty tensor, LayerNorm(h) if weight is given else an empty tensor)."""
+    dev = _require_gpu(*[t for t in (x, y, gamma, weight, bias) if t is not None])
+    C = x.shape[-1]
+    for name, t in (("x", x), ("y", y), ("gamma", gamma), ("weight", weight), ("bias", bias)):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"gpa::residual_layernorm takes bf16 {name}, got {t.dtype}")
+    if y is not None and (y.shape != x.shape or gamma is None or gamma.shape != (C,)):
+        raise ValueError("gpa::residual_layernorm: y must match x and gamma be [C]")
+    if weight is not None and (bias is None or weight.shape != (C,) or bias.shape != (C,)):
+        raise ValueError("gpa::residual_layernorm: weight and bias must be [C]")
+    if want_h and y is None:
+        raise ValueError("gpa::residual_layernorm: want_h needs y")
+    xr = x.reshape(-1, C)
+    if not _rows_ok(xr, 8):
+        xr = xr.contiguous()
+    yr = None
+    if y is not None:
+        yr = y.reshape(-1, C)
+        if not _rows_ok(yr, 8):
+            yr = yr.contiguous()
+        gamma = gamma.contiguous()
+    if weight is not None:
+        weight, bias = weight.contiguous(), bias.contiguous()
+    rows = xr.shape[0]
+    h = torch.empty(x.shape, device=dev, dtype=torch.bfloat16) if want_h else x.new_empty(0)
+    ln = torch.empty(x.shape, device=dev, dtype=torch.bfloat16) if weight is not None \
+        else x.new_empty(0)
+    if rows == 0:
+        return h, ln
+    with torch.cuda.device(dev):
+        rc = lib().gpa_residual_layernorm_bf16(
+            xr.data_ptr(), None if yr is None else yr.data_ptr(),
+            None if gamma is None else gamma.data_ptr(),
+            None if weight is None else weight.data_ptr(),
+            None if bias is None else bias.data_ptr(), float(eps), rows, C,
+            _rs(xr, 0), 0 if yr is None else _rs(yr, 0),
+            h.data_ptr() if want_h else None, C, ln.data_ptr() if weight is not None else None, C,
+            _stream(dev))
+    _check(rc, "gpa::residual_layernorm")
+    return h, ln
+
+
+@residual_layernorm.register_fake
+def _residual_layernorm_fake(x, y, gamma, weight, bias, eps, want_h):
+    return (x.new_empty(x.shape if want_h else (0,)),
+            x.new_empty(x.shape if weight is not None else (0,)))

@@ -1,7 +1,7 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Seven entry points (two of them with an fp16 twin) sit behind this
+ * Eight entry points (two of them with an fp16 twin) sit behind this
  * boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
@@ -23,6 +23,9 @@
  *                           K/V set (replaces vggt/layers/attention.py:113-140).
  *   gpa_merge_metric_bf16 — the merge's metric projection, normalisation and
  *                           dst/src split (replaces merging/merge.py:180-187).
+ *   gpa_residual_layernorm_bf16 — residual + LayerScale + LayerNorm of the
+ *                           caller's blocks (replaces vggt/layers/block.py:84-96
+ *                           torch ops).
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
@@ -46,7 +49,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 7
+#define GPA_ABI_VERSION 8
 
 enum {
   GPA_OK = 0,
@@ -276,6 +279,24 @@ int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* poo
 int gpa_merge_metric_bf16(const void* metric, int metric_dtype, int64_t B, int64_t N, int64_t C,
                           int64_t m_sb, int64_t m_sn, const void* proj, int64_t P,
                           const int64_t* order, int norm_mode, void* out, void* stream);
+
+/*
+ * Residual + LayerScale + LayerNorm of a pre-LN block, bf16 rows of C
+ * features (C a multiple of 512, <= 4096), one pass:
+ *   h   = bf16(x + bf16(gamma * y))                     (y given; else h = x)
+ *   out = bf16((h - mean) * rsqrt(var + eps) * w + b)    fp32 moments, biased var
+ * h_out (only with y) and ln_out are each optional, but one is required.
+ * Rows are x + r*x_sn (likewise y, h_out, ln_out); rows and gamma / w / b
+ * 16-byte aligned.  Replaces `x + self.ls1(attn_out)` / `self.norm2(x)` of
+ * vggt/layers/block.py:84-96 under bf16 autocast (bf16 multiply and add,
+ * fp32 layer_norm, the cast to bf16 before the next Linear); the reference
+ * module interface has no such entry point (it runs these as torch ops).
+ */
+int gpa_residual_layernorm_bf16(const void* x, const void* y, const void* gamma,
+                                const void* ln_weight, const void* ln_bias, float eps,
+                                int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn,
+                                void* h_out, int64_t h_sn, void* ln_out, int64_t ln_sn,
+                                void* stream);
 
 #ifdef __cplusplus
 }

@@ -245,6 +245,34 @@ def test_merge_metric_empty_is_a_no_op():
     assert _metric(N=0) == _native.GPA_OK
 
 
+def _rln(**kw):
+    args = dict(x=FAKE, y=FAKE, gamma=FAKE, w=FAKE, b=FAKE, eps=1e-6, rows=10, C=1024, x_sn=1024,
+                y_sn=1024, h=FAKE, h_sn=1024, ln=FAKE, ln_sn=1024, stream=None)
+    args.update(kw)
+    return _native.lib().gpa_residual_layernorm_bf16(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(rows=-1), _native.GPA_E_INVALID),
+    (dict(C=1000, x_sn=1000), _native.GPA_E_UNSUPPORTED),      # not a multiple of 512
+    (dict(C=8192), _native.GPA_E_UNSUPPORTED),
+    (dict(x=None), _native.GPA_E_INVALID),
+    (dict(gamma=None), _native.GPA_E_INVALID),                  # y without gamma
+    (dict(w=None), _native.GPA_E_INVALID),                      # ln_out without weight
+    (dict(h=None, ln=None), _native.GPA_E_INVALID),             # no output
+    (dict(y=None), _native.GPA_E_INVALID),                      # h_out without y
+    (dict(eps=float("nan")), _native.GPA_E_INVALID),
+    (dict(x_sn=1020), _native.GPA_E_INVALID),                   # misaligned rows
+])
+def test_residual_layernorm_argument_errors(kw, code):
+    assert _rln(**kw) == code
+    assert _native.lib().gpa_last_error()
+
+
+def test_residual_layernorm_empty_is_a_no_op():
+    assert _rln(rows=0) == _native.GPA_OK
+
+
 @pytest.mark.parametrize("frames,w,h,sx,sy,ns,no_rand", [
     (6, 37, 37, 2, 2, 5, False), (5, 7, 5, 2, 2, 5, False), (3, 9, 9, 3, 3, 1, False),
     (4, 6, 6, 2, 2, 5, True), (1, 6, 6, 2, 2, 5, False), (3, 10, 4, 3, 2, 2, False),
