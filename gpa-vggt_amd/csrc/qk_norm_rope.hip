@@ -24,8 +24,10 @@
 // Work split: eight lanes own one (token, head, q|k) row, 16 bytes each;
 // the LayerNorm moments and the rotation partner (feature j <-> j+16 is lane
 // c <-> c^2 within the eight) are cross-lane exchanges.  A workgroup handles
-// 32 consecutive tokens of one (q|k, head), so its writes are one contiguous
-// 4 KB (bf16) run.  HBM-bound.
+// 128 consecutive tokens of one (q|k, head), four rows per lane group, all
+// four loads issued before any arithmetic (one 16-byte load per lane in
+// flight held the kernel to ~3 TB/s); each pass of the group's 32 rows
+// writes one contiguous 4 KB (bf16) run.  HBM-bound.
 #include "gpa_common.h"
 
 namespace gpa {
@@ -33,7 +35,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLanesPerRow = 8;
-constexpr int kRowsPerBlock = kThreads / kLanesPerRow;
+constexpr int kRowsPerPass = kThreads / kLanesPerRow;   // 32
+constexpr int kPasses = 4;
+constexpr int kRowsPerBlock = kRowsPerPass * kPasses;
 constexpr int kHeadDim = 64;
 
 struct QkArgs {
@@ -64,60 +68,73 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
   const int which = blockIdx.y & 1;            // 0: q, 1: k
   const int64_t h = blockIdx.y >> 1;
   const int c = threadIdx.x % kLanesPerRow;    // features 8c .. 8c+7
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
-  const bool valid = row < a.rows;
-  const int64_t rc = valid ? row : a.rows - 1;  // every lane joins the exchanges
-  const int64_t b = rc / a.N, n = rc % a.N;
+  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
 
-  const bf16x8 xv = *reinterpret_cast<const bf16x8*>(
-      a.qkv + b * a.sb + n * a.sn + which * a.k_offset + h * kHeadDim + c * 8);
-  float x[8];
+  bf16x8 xv[kPasses];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = (float)xv[i];
-
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) s += x[i];
-  const float mean = group_sum8(s) * (1.0f / kHeadDim);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    x[i] -= mean;
-    ss += x[i] * x[i];
+  for (int r = 0; r < kPasses; ++r) {
+    const int64_t row = row0 + r * kRowsPerPass;
+    const int64_t rc = row < a.rows ? row : a.rows - 1;   // every lane joins the exchanges
+    const int64_t b = rc / a.N, n = rc % a.N;
+    xv[r] = *reinterpret_cast<const bf16x8*>(a.qkv + b * a.sb + n * a.sn + which * a.k_offset +
+                                             h * kHeadDim + c * 8);
   }
-  const float rstd = rsqrtf(group_sum8(ss) * (1.0f / kHeadDim) + a.eps);
   const float* w = a.w + which * kHeadDim + c * 8;
   const float* be = a.beta + which * kHeadDim + c * 8;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = x[i] * rstd * w[i] + be[i];
+  void* out = which ? a.k_out : a.q_out;
+  const bool out_f32 = which ? a.k_f32 : a.q_f32;
 
-  if (a.pos != nullptr) {
-    int p = a.pos[(n % a.period) * 2 + (c >= 4 ? 1 : 0)];
-    p = p < 0 ? 0 : (p >= a.npos ? a.npos - 1 : p);
-    const float sgn = (c & 2) ? 1.0f : -1.0f;   // second quarter of a half: +, first: -
-    const float2* cs = reinterpret_cast<const float2*>(a.cs) + (int64_t)p * 16 + (c & 1) * 8;
-    float partner[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) partner[i] = __shfl_xor(x[i], 2);
+  for (int r = 0; r < kPasses; ++r) {
+    const int64_t row = row0 + r * kRowsPerPass;
+    const bool valid = row < a.rows;
+    const int64_t rc = valid ? row : a.rows - 1;
+    const int64_t b = rc / a.N, n = rc % a.N;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (float)xv[r][i];
+
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += x[i];
+    const float mean = group_sum8(s) * (1.0f / kHeadDim);
+    float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float2 t = cs[i];
-      x[i] = __builtin_fmaf(x[i], t.x, sgn * partner[i] * t.y);
+      x[i] -= mean;
+      ss += x[i] * x[i];
     }
-  }
-  if (!valid) return;
-
-  const int64_t o = ((b * a.H + h) * a.N + n) * kHeadDim + c * 8;
-  void* out = which ? a.k_out : a.q_out;
-  if (which ? a.k_f32 : a.q_f32) {
-    f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(out) + o);
-    dst[0] = f32x4{x[0], x[1], x[2], x[3]};
-    dst[1] = f32x4{x[4], x[5], x[6], x[7]};
-  } else {
-    bf16x8 yv;
+    const float rstd = rsqrtf(group_sum8(ss) * (1.0f / kHeadDim) + a.eps);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) yv[i] = (__bf16)x[i];
-    *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + o) = yv;
+    for (int i = 0; i < 8; ++i) x[i] = x[i] * rstd * w[i] + be[i];
+
+    if (a.pos != nullptr) {
+      int p = a.pos[(n % a.period) * 2 + (c >= 4 ? 1 : 0)];
+      p = p < 0 ? 0 : (p >= a.npos ? a.npos - 1 : p);
+      const float sgn = (c & 2) ? 1.0f : -1.0f;   // second quarter of a half: +, first: -
+      const float2* cs = reinterpret_cast<const float2*>(a.cs) + (int64_t)p * 16 + (c & 1) * 8;
+      float partner[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) partner[i] = __shfl_xor(x[i], 2);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float2 t = cs[i];
+        x[i] = __builtin_fmaf(x[i], t.x, sgn * partner[i] * t.y);
+      }
+    }
+    if (!valid) continue;
+
+    const int64_t o = ((b * a.H + h) * a.N + n) * kHeadDim + c * 8;
+    if (out_f32) {
+      f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(out) + o);
+      dst[0] = f32x4{x[0], x[1], x[2], x[3]};
+      dst[1] = f32x4{x[4], x[5], x[6], x[7]};
+    } else {
+      bf16x8 yv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) yv[i] = (__bf16)x[i];
+      *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + o) = yv;
+    }
   }
 }
 
