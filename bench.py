@@ -338,7 +338,7 @@ def main(argv=None) -> int:
         order = torch.argsort(dst_mask(S, 37, 37, 2, 2, pts, False, g, dev), stable=True)
         metric = torch.randn(1, S * P, 1024, device=dev)
         proj = _projection(dev, 1024, 128)
-        fn = lambda: _native.merge_metric(metric, proj, order, False)  # noqa: E731
+        fn = lambda: _native.merge_metric(metric, proj, order, 0)  # noqa: E731
         fn()
         t = statistics.median(event_ms(fn, 5))
         nbytes = S * P * (1024 * 4 + 128 * 2)

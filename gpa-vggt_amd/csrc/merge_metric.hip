@@ -14,7 +14,10 @@
 // 90-95).  With `order` = [dst positions | src positions] the output holds b
 // followed by a, in the layout the similarity kernel reads.  Mode 1 is the
 // same chain without autocast on a bf16 metric: there the norm comes back in
-// bf16 before the division.  There is no epsilon: a zero row gives NaN, as
+// bf16 before the division.  Mode 2 is the chain under fp16 autocast: the
+// metric and the projection are rounded to fp16, the product runs on the
+// fp16 MFMA and y is rounded to fp16 (the norm, the division and the final
+// bf16 cast as in mode 0).  There is no epsilon: a zero row gives NaN, as
 // in the reference.
 //
 // Design: HBM-bound (one read of the metric, 4 KB per token in fp32, and a
@@ -54,8 +57,22 @@ struct MetricArgs {
 
 __device__ __forceinline__ float bf16r(float x) { return (float)(__bf16)x; }
 
-template <int C, bool F32>
+// The projection's rounding: bf16, or fp16 under fp16 autocast.  The empty
+// asm keeps the fp16 round trip a real rounding step.
+template <bool P16>
+__device__ __forceinline__ float proj_round(float x) {
+  if constexpr (P16) {
+    uint32_t u = __builtin_bit_cast(uint16_t, (_Float16)x);
+    asm volatile("" : "+v"(u));
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+  } else {
+    return bf16r(x);
+  }
+}
+
+template <int C, bool F32, bool P16>
 __global__ __launch_bounds__(kThreads, 1) void merge_metric_kernel(MetricArgs a) {
+  static_assert(F32 || !P16, "the fp16 projection takes an fp32 metric");
   constexpr int kSteps = C / 32;                         // MFMA k-steps
   constexpr int kSpan = F32 ? 4 : 8;                     // elements per 16-byte load
   constexpr int kLoads = C / (32 * kSpan);               // loads per thread per row
@@ -103,7 +120,7 @@ __global__ __launch_bounds__(kThreads, 1) void merge_metric_kernel(MetricArgs a)
       if constexpr (F32) {                                 // chunk l*16 + (lc >> 1)
         bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (__bf16)raw[l][e];
+        for (int e = 0; e < 4; ++e) v[e] = f32_to_half<P16>(raw[l][e]);
         *reinterpret_cast<bf16x4*>(st_base + l * 128) = v;
       } else {                                             // chunk l*32 + lc
         *reinterpret_cast<bf16x8*>(st_base + l * 256) = raw[l];
@@ -116,7 +133,7 @@ __global__ __launch_bounds__(kThreads, 1) void merge_metric_kernel(MetricArgs a)
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) {
       const bf16x8 af = *reinterpret_cast<const bf16x8*>(rd_base[ks & 3] + (ks >> 2) * 128);
-      acc[ks & 3] = mfma16x16x32(af, __builtin_bit_cast(bf16x8, bfrag[ks]), acc[ks & 3]);
+      acc[ks & 3] = mfma16x16x32_t<P16>(af, __builtin_bit_cast(bf16x8, bfrag[ks]), acc[ks & 3]);
     }
     // At most four A fragments in flight: the resident projection leaves no
     // room for the compiler's habit of issuing every LDS read up front.
@@ -130,7 +147,7 @@ __global__ __launch_bounds__(kThreads, 1) void merge_metric_kernel(MetricArgs a)
     float y[4], s[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      y[r] = bf16r((acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]));   // row 4g + r
+      y[r] = proj_round<P16>((acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]));   // row 4g + r
       s[r] = y[r] * y[r];
 #pragma unroll
       for (int m = 1; m < 16; m <<= 1) s[r] += __shfl_xor(s[r], m);
@@ -180,11 +197,13 @@ int cu_count() {
 }
 
 template <int C>
-void launch(bool f32, dim3 grid, hipStream_t s, const MetricArgs& a) {
-  if (f32)
-    hipLaunchKernelGGL((merge_metric_kernel<C, true>), grid, dim3(kThreads), 0, s, a);
+void launch(bool f32, bool p16, dim3 grid, hipStream_t s, const MetricArgs& a) {
+  if (p16)
+    hipLaunchKernelGGL((merge_metric_kernel<C, true, true>), grid, dim3(kThreads), 0, s, a);
+  else if (f32)
+    hipLaunchKernelGGL((merge_metric_kernel<C, true, false>), grid, dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((merge_metric_kernel<C, false>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((merge_metric_kernel<C, false, false>), grid, dim3(kThreads), 0, s, a);
 }
 
 }  // namespace
@@ -205,9 +224,13 @@ extern "C" int gpa_merge_metric_bf16(const void* metric, int metric_dtype, int64
     gpa_set_error("gpa_merge_metric_bf16: metric dtype %d is not fp32 or bf16", metric_dtype);
     return GPA_E_UNSUPPORTED;
   }
-  if (norm_mode != 0 && norm_mode != 1) {
-    gpa_set_error("gpa_merge_metric_bf16: norm_mode %d is not 0 or 1", norm_mode);
+  if (norm_mode < 0 || norm_mode > 2) {
+    gpa_set_error("gpa_merge_metric_bf16: norm_mode %d is not 0, 1 or 2", norm_mode);
     return GPA_E_INVALID;
+  }
+  if (norm_mode == 2 && metric_dtype != GPA_DTYPE_F32) {
+    gpa_set_error("gpa_merge_metric_bf16: the fp16 projection (norm_mode 2) takes an fp32 metric");
+    return GPA_E_UNSUPPORTED;
   }
   if (P != kOut || (C != 256 && C != 512 && C != 768 && C != 1024)) {
     gpa_set_error("gpa_merge_metric_bf16: projection %lld -> %lld unsupported (C in "
@@ -242,16 +265,16 @@ extern "C" int gpa_merge_metric_bf16(const void* metric, int metric_dtype, int64
   a.N = N;
   a.rows = B * N;
   a.nblocks = (int)nblocks;
-  a.norm_bf16 = norm_mode;
+  a.norm_bf16 = norm_mode == 1;
   const int64_t g = nblocks < cu_count() ? nblocks : cu_count();
   const bool f32 = metric_dtype == GPA_DTYPE_F32;
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)g);
   switch (C) {
-    case 256: launch<256>(f32, grid, s, a); break;
-    case 512: launch<512>(f32, grid, s, a); break;
-    case 768: launch<768>(f32, grid, s, a); break;
-    default: launch<1024>(f32, grid, s, a); break;
+    case 256: launch<256>(f32, norm_mode == 2, grid, s, a); break;
+    case 512: launch<512>(f32, norm_mode == 2, grid, s, a); break;
+    case 768: launch<768>(f32, norm_mode == 2, grid, s, a); break;
+    default: launch<1024>(f32, norm_mode == 2, grid, s, a); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

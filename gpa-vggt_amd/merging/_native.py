@@ -563,20 +563,25 @@ _METRIC_DTYPES = {torch.float32: GPA_DTYPE_F32, torch.bfloat16: GPA_DTYPE_BF16}
 
 @torch.library.custom_op("gpa::merge_metric", mutates_args=())
 def merge_metric(metric: torch.Tensor, proj: torch.Tensor, order: Optional[torch.Tensor],
-                 norm_bf16: bool) -> torch.Tensor:
-    """bf16(normalise(bf16(bf16(metric[:, order]) @ proj))) as [B, N, 128] bf16.
+                 mode: int) -> torch.Tensor:
+    """bf16(normalise(round(round(metric[:, order]) @ proj))) as [B, N, 128] bf16.
 
-    metric [B, N, C] fp32 or bf16 (C in 256, 512, 768, 1024), proj [C, 128]
-    bf16, order [N] int64 token positions (None: identity).  norm_bf16 rounds
-    the row norm to bf16 before the division (the chain without autocast)."""
+    metric [B, N, C] fp32 or bf16 (C in 256, 512, 768, 1024), order [N] int64
+    token positions (None: identity).  mode 0: bf16 projection (proj [C, 128]
+    bf16), fp32 norm -- the chain under bf16 autocast; 1: the same with the
+    norm rounded to bf16 -- a bf16 metric without autocast; 2: fp16 projection
+    (proj fp16, fp32 metric), fp32 norm -- the chain under fp16 autocast."""
     dev = _require_gpu(metric, proj)
     if metric.dim() != 3 or metric.dtype not in _METRIC_DTYPES:
         raise ValueError(f"gpa::merge_metric: metric must be fp32/bf16 [B,N,C], got "
                          f"{metric.dtype} {tuple(metric.shape)}")
+    if mode not in (0, 1, 2):
+        raise ValueError(f"gpa::merge_metric: mode {mode} is not 0, 1 or 2")
     B, N, C = metric.shape
-    if proj.dtype != torch.bfloat16 or proj.dim() != 2 or proj.shape[0] != C:
-        raise ValueError(f"gpa::merge_metric: proj must be bf16 [{C}, P], got {proj.dtype} "
-                         f"{tuple(proj.shape)}")
+    want = torch.float16 if mode == 2 else torch.bfloat16
+    if proj.dtype != want or proj.dim() != 2 or proj.shape[0] != C:
+        raise ValueError(f"gpa::merge_metric: mode {mode} takes a {want} proj [{C}, P], got "
+                         f"{proj.dtype} {tuple(proj.shape)}")
     P = proj.shape[1]
     proj = proj.contiguous()
     if order is not None:
@@ -594,13 +599,13 @@ def merge_metric(metric: torch.Tensor, proj: torch.Tensor, order: Optional[torch
         rc = lib().gpa_merge_metric_bf16(
             metric.data_ptr(), _METRIC_DTYPES[metric.dtype], B, N, C, _st(metric, 0),
             _rs(metric, 1), proj.data_ptr(), P, None if order is None else order.data_ptr(),
-            1 if norm_bf16 else 0, out.data_ptr(), _stream(dev))
+            int(mode), out.data_ptr(), _stream(dev))
     _check(rc, "gpa::merge_metric")
     return out
 
 
 @merge_metric.register_fake
-def _merge_metric_fake(metric, proj, order, norm_bf16):
+def _merge_metric_fake(metric, proj, order, mode):
     B, N, _ = metric.shape
     return metric.new_empty(B, N, proj.shape[1], dtype=torch.bfloat16)
 

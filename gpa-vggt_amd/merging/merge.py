@@ -14,9 +14,10 @@ Orderings the reference leaves to torch's sort are fixed here:
 These are the orders torch's GPU radix sort produces for such inputs.
 `merge.index` exposes the index tensors for inspection.
 
-Under bf16 autocast (the model's case), or on a bf16 metric, the metric
-projection, normalisation, dst/src split and bf16 cast (reference :180-187
-and fused_similarity.py:90-95) run as one gfx950 kernel
+Under bf16 or fp16 autocast (the model's and the evaluation stack's
+cases), or on a bf16 metric, the metric projection, normalisation, dst/src
+split and bf16 cast (reference :180-187 and fused_similarity.py:90-95) run
+as one gfx950 kernel
 (`gpa::merge_metric`) that writes the similarity operands [dst | src]
 directly; node_max keeps the dtype the reference's division yields (fp32
 under autocast).  Other chains (fp32 arithmetic without autocast, no
@@ -117,13 +118,17 @@ def _projection(dev: torch.device, C: int, metric_dim: int,
 def _front_end_mode(metric: torch.Tensor, C: int, metric_dim: int) -> Optional[str]:
     """Which rounding chain the fused front end reproduces, or None when the
     reference's chain is one the kernel does not compute (no projection, a
-    projection other than C -> 128, fp32 arithmetic without autocast, fp16)."""
+    projection other than C -> 128, fp32 arithmetic without autocast, a
+    non-fp32 metric under fp16 autocast)."""
     if metric_dim != 128 or C not in (256, 512, 768, 1024):
         return None
     if torch.is_autocast_enabled("cuda"):
-        if torch.get_autocast_dtype("cuda") != torch.bfloat16:
-            return None
-        return "autocast" if metric.dtype in (torch.float32, torch.bfloat16) else None
+        dt = torch.get_autocast_dtype("cuda")
+        if dt == torch.bfloat16:
+            return "autocast" if metric.dtype in (torch.float32, torch.bfloat16) else None
+        if dt == torch.float16:
+            return "autocast16" if metric.dtype == torch.float32 else None
+        return None
     return "bf16" if metric.dtype == torch.bfloat16 else None
 
 
@@ -178,9 +183,12 @@ def token_merge_bipartite2d(
             # bf16 cast (reference :180-187 plus the cast of
             # fused_similarity.py:90-95); node_max keeps the dtype the
             # reference's division produces.
-            ab = _native.merge_metric(metric, _projection(dev, C, metric_dim), order,
-                                      front == "bf16")
-            max_dtype = torch.float32 if front == "autocast" else torch.bfloat16
+            mode = {"autocast": 0, "bf16": 1, "autocast16": 2}[front]
+            ab = _native.merge_metric(
+                metric, _projection(dev, C, metric_dim,
+                                    torch.float16 if mode == 2 else torch.bfloat16),
+                order, mode)
+            max_dtype = torch.bfloat16 if front == "bf16" else torch.float32
             a = ab[:, num_dst:]
             b = ab[:, :num_dst]
         else:

@@ -75,7 +75,7 @@ def main(argv=None) -> int:
         metric = torch.randn(1, 200 * 1374, 1024, device=dev)
         proj = _projection(dev, 1024, 128)
         for _ in range(reps):
-            _native.merge_metric(metric, proj, order, False)
+            _native.merge_metric(metric, proj, order, 0)
         torch.cuda.synchronize()
         print(f"front 274800x1024 f32 -> 128 x {reps} done", flush=True)
         del metric, order

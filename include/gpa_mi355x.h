@@ -265,6 +265,9 @@ int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* poo
  *   y = bf16( bf16(metric[b, t, :]) @ proj )   C -> P, fp32 accumulation
  *   n = sqrt(sum y^2) in fp32; norm_mode 1 rounds n to bf16
  *   out[b, j, :] = bf16(y / n)                  (no epsilon: a zero row gives NaN)
+ * norm_mode 2 is the chain under fp16 autocast: the metric (fp32 only) and
+ * proj (then fp16 bits) are rounded to fp16, y = fp16(...) on the fp16 MFMA,
+ * and n, the division and the output as in mode 0.
  * metric: [B, N, C] of metric_dtype (GPA_DTYPE_F32 or GPA_DTYPE_BF16), unit
  * feature stride, 16-byte aligned rows, C in {256, 512, 768, 1024}; proj:
  * contiguous [C][P] bf16, P = 128; order: int64 [N]; out: contiguous

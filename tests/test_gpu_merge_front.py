@@ -26,9 +26,9 @@ from oracle.similarity import bf16_top2_gap
 pytestmark = pytest.mark.gpu
 
 
-def _torch_chain(metric, proj_f32, order, autocast):
+def _torch_chain(metric, proj_f32, order, autocast, dtype=torch.bfloat16):
     if autocast:
-        with torch.autocast("cuda", dtype=torch.bfloat16):
+        with torch.autocast("cuda", dtype=dtype):
             m = metric @ proj_f32.to(metric.dtype)
             m = m / m.norm(dim=-1, keepdim=True)
         return m.index_select(1, order).to(torch.bfloat16)
@@ -38,8 +38,9 @@ def _torch_chain(metric, proj_f32, order, autocast):
 
 
 def _fp64_chain(metric, proj_bf16, order, norm_bf16):
-    x = metric.to(torch.bfloat16).double().cpu()[:, order.cpu()]
-    y = (x @ proj_bf16.double().cpu()).to(torch.bfloat16).double()
+    rnd = proj_bf16.dtype                  # bf16, or fp16 for the fp16-autocast chain
+    x = metric.to(rnd).double().cpu()[:, order.cpu()]
+    y = (x @ proj_bf16.double().cpu()).to(rnd).double()
     n = y.norm(dim=-1, keepdim=True)
     if norm_bf16:
         n = n.to(torch.bfloat16).double()
@@ -89,9 +90,9 @@ def test_vggt_width_against_the_chain(dev, dtype, autocast):
     proj = _projection(dev, 1024, 128)
     if autocast:
         with torch.autocast("cuda", dtype=torch.bfloat16):
-            got = _native.merge_metric(metric, proj, order, False)
+            got = _native.merge_metric(metric, proj, order, 0)
     else:
-        got = _native.merge_metric(metric, proj, order, True)
+        got = _native.merge_metric(metric, proj, order, 1)
     chain = _torch_chain(metric, proj_f32, order, autocast)
     assert got.dtype == torch.bfloat16 and got.shape == (1, metric.shape[1], 128)
     _compare(got, chain, _fp64_chain(metric, proj, order, not autocast), f"{dtype} {autocast}")
@@ -109,7 +110,7 @@ def test_widths_batches_strides_and_tails(dev, C):
     proj = proj_f32.to(torch.bfloat16)
     for order in (torch.randperm(N, generator=g).to(dev), None):
         with torch.autocast("cuda", dtype=torch.bfloat16):
-            got = _native.merge_metric(metric, proj, order, False)
+            got = _native.merge_metric(metric, proj, order, 0)
         o = torch.arange(N, device=dev) if order is None else order
         chain = _torch_chain(metric, proj_f32, o, True)
         _compare(got, chain, _fp64_chain(metric, proj, o, False), f"C={C}")
@@ -123,7 +124,7 @@ def test_many_blocks_per_workgroup(dev):
     order = torch.randperm(N, generator=g).to(dev)
     proj_f32 = _projection(dev, C, 128, torch.float32)
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        got = _native.merge_metric(metric, _projection(dev, C, 128), order, False)
+        got = _native.merge_metric(metric, _projection(dev, C, 128), order, 0)
     chain = _torch_chain(metric, proj_f32, order, True)
     ulps = (_ordered(got) - _ordered(chain)).abs()
     assert (ulps > 0).float().mean().item() <= 2e-3
@@ -131,7 +132,7 @@ def test_many_blocks_per_workgroup(dev):
             + ABS_FLOOR).all()
     # Deterministic: the row sums meet in a fixed order.
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        again = _native.merge_metric(metric, _projection(dev, C, 128), order, False)
+        again = _native.merge_metric(metric, _projection(dev, C, 128), order, 0)
     assert torch.equal(got, again)
 
 
@@ -140,7 +141,7 @@ def test_zero_row_gives_nan_like_the_reference(dev):
     metric[0, 7] = 0
     proj = torch.randn(256, 128, device=dev).to(torch.bfloat16)
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        got = _native.merge_metric(metric, proj, None, False)
+        got = _native.merge_metric(metric, proj, None, 0)
     assert torch.isnan(got[0, 7]).all()
     assert torch.isfinite(got[0, torch.arange(40, device=dev) != 7]).all()
 
@@ -168,3 +169,40 @@ def test_token_merge_uses_the_front_end_under_autocast(dev):
     assert torch.equal(ix.node_idx[keep], ref_idx[keep])
     assert (ix.node_max - ref_max).abs().max().item() < 2e-2
     assert m.size.sum().item() == n
+
+
+def test_fp16_autocast_chain(dev):
+    """Mode 2: under fp16 autocast the projection runs in fp16 (metric and
+    basis rounded to fp16, y rounded to fp16), then the fp32 norm and the
+    bf16 cast of the similarity operands."""
+    frames = 4
+    metric = W.shifted_basis_tokens(frames, seed=8).to(dev)            # fp32
+    order = _order(frames, dev)
+    proj_f32 = _projection(dev, 1024, 128, torch.float32)
+    proj16 = _projection(dev, 1024, 128, torch.float16)
+    got = _native.merge_metric(metric, proj16, order, 2)
+    chain = _torch_chain(metric, proj_f32, order, True, torch.float16)
+    _compare(got, chain, _fp64_chain(metric, proj16, order, False), "fp16 autocast")
+    with pytest.raises(ValueError):
+        _native.merge_metric(metric, _projection(dev, 1024, 128), order, 2)   # bf16 basis
+
+
+def test_token_merge_under_fp16_autocast(dev):
+    frames, ns = 4, 5
+    metric = W.shifted_basis_tokens(frames, seed=9).to(dev)
+    n = metric.shape[1]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(33)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        m = token_merge_bipartite2d(metric, 37, 37, 2, 2, int(0.98 * n), False, gen,
+                                    metric_dim=128, num_special=ns)
+    ix = m.index
+    assert ix.node_max.dtype == torch.float32
+    num_dst = num_dst_tokens(frames, 37, 37, 2, 2, ns, False)
+    order = torch.cat([ix.b_idx, ix.a_idx])
+    ab = _torch_chain(metric, _projection(dev, 1024, 128, torch.float32), order, True,
+                      torch.float16)
+    a, b = ab[:, num_dst:], ab[:, :num_dst]
+    _, ref_idx = torch.ops.gpa.sim_argmax(a, b)
+    keep = (bf16_top2_gap(a, b) >= 1e-3).to(dev)
+    assert torch.equal(ix.node_idx[keep], ref_idx[keep])

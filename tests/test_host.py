@@ -228,7 +228,8 @@ def _metric(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(N=-1), _native.GPA_E_INVALID),
     (dict(dt=2), _native.GPA_E_UNSUPPORTED),                # fp16 metric
-    (dict(mode=2), _native.GPA_E_INVALID),
+    (dict(mode=3), _native.GPA_E_INVALID),
+    (dict(mode=2, dt=_native.GPA_DTYPE_BF16), _native.GPA_E_UNSUPPORTED),   # fp16 projection: fp32 metric
     (dict(C=1000, sn=1000), _native.GPA_E_UNSUPPORTED),     # C not in {256, 512, 768, 1024}
     (dict(P=64), _native.GPA_E_UNSUPPORTED),
     (dict(x=None), _native.GPA_E_INVALID),
