@@ -120,11 +120,11 @@ struct RecArgs {
   const uint16_t* k;
   const void* bias;
   float* recs;
-  int kind;
   int H;
   int64_t k_sb, k_sh, k_sn;
   int64_t sb, sh, sn;  // bias strides (0 = broadcast)
   int64_t N, ntiles;
+  int64_t total;  // B * H * ntiles
   float mul;  // 1 / sm_scale
   float c;    // sm_scale * log2(e)
 };
@@ -168,58 +168,94 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Tile records: one workgroup per 32-key tile, eight lanes per key row (one
-// 16-byte chunk each), so a wave's loads cover eight whole 128-byte rows
-// and the rows stream at HBM rate.  The lanes of a key reduce its |k|^2;
-// the tile's two maxima meet across the wave (xor 8, 16, 32) and then the
-// four waves in LDS.  Keys past N get bias -inf and |k| = 0.
-template <bool F16>
+// Tile records: one workgroup per kRecTiles consecutive 32-key tiles, eight
+// lanes per key row (one 16-byte chunk each), so a wave's loads cover eight
+// whole 128-byte rows.  Every lane issues its kRecTiles row loads (and bias
+// loads) before it reduces any of them, which keeps 16 KB in flight per
+// workgroup: with one tile per workgroup the kernel waited out one memory
+// round trip per 4 KB.  The lanes of a key reduce its |k|^2; a tile's two
+// maxima meet across the wave (xor 8, 16, 32) and then across the four
+// waves in LDS.  Keys past N get bias -inf and |k| = 0; tiles past the last
+// (batch, head) row are skipped.
+constexpr int kRecTiles = 4;
+
+// Bias bits of one key (uniform kind; no bias reads as 0).
+template <int KIND>
+__device__ __forceinline__ uint32_t bias_bits(const void* bias, int64_t off) {
+  if constexpr (KIND == GPA_BIAS_F32) return static_cast<const uint32_t*>(bias)[off];
+  else if constexpr (KIND == GPA_BIAS_NONE) return 0u;
+  else return static_cast<const uint16_t*>(bias)[off];
+}
+template <int KIND>
+__device__ __forceinline__ float bias_value(uint32_t bits) {
+  if constexpr (KIND == GPA_BIAS_F32) return __uint_as_float(bits);
+  else if constexpr (KIND == GPA_BIAS_BF16) return bf16_bits_to_f32((uint16_t)bits);
+  else if constexpr (KIND == GPA_BIAS_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+  else return 0.f;
+}
+
+template <bool F16, int KIND>
 __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
-  __shared__ float part[2][4];
+  __shared__ float part[kRecTiles][2][4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t tile = blockIdx.x;                     // over B*H*ntiles
-  const int64_t row = tile / a.ntiles, t = tile % a.ntiles;
-  const int64_t hb = row % a.H, bb = row / a.H;
   const int j = tid >> 3, ch = tid & 7;                // key of the tile, 16-byte chunk
-  const int64_t n = t * kKT + j;
-  float x = -INFINITY, ss = 0.f;
-  if (n < a.N) {
-    const int64_t off = bb * a.sb + hb * a.sh + n * a.sn;
-    if (a.kind == GPA_BIAS_F32)
-      x = static_cast<const float*>(a.bias)[off] * a.mul;
-    else if (a.kind == GPA_BIAS_BF16)
-      x = bf16_bits_to_f32(static_cast<const uint16_t*>(a.bias)[off]) * a.mul;
-    else if (a.kind == GPA_BIAS_F16)
-      x = (float)static_cast<const _Float16*>(a.bias)[off] * a.mul;
-    else
-      x = 0.f;
-    const bf16x8 v =
-        *reinterpret_cast<const bf16x8*>(a.k + bb * a.k_sb + hb * a.k_sh + n * a.k_sn + ch * 8);
+  const int64_t tile0 = (int64_t)blockIdx.x * kRecTiles;
+  const int64_t row0 = tile0 / a.ntiles;
+  int64_t t = tile0 - row0 * a.ntiles, hb = row0 % a.H, bb = row0 / a.H;
+  // All loads first, without branches: a key that does not exist (past N,
+  // or in a tile past the last row) reads element 0 of K and of the bias
+  // instead and is masked afterwards.
+  bf16x8 kv[kRecTiles];
+  uint32_t xb[kRecTiles];
+  bool live[kRecTiles];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = half_to_f32<F16>(v[e]);
-      ss = __builtin_fmaf(f, f, ss);
+  for (int u = 0; u < kRecTiles; ++u) {
+    const int64_t n = t * kKT + j;
+    live[u] = tile0 + u < a.total && n < a.N;
+    const int64_t koff = live[u] ? bb * a.k_sb + hb * a.k_sh + n * a.k_sn : 0;
+    const int64_t boff = live[u] ? bb * a.sb + hb * a.sh + n * a.sn : 0;
+    kv[u] = *reinterpret_cast<const bf16x8*>(a.k + koff + ch * 8);
+    xb[u] = bias_bits<KIND>(a.bias, boff);
+    if (++t == a.ntiles) {
+      t = 0;
+      if (++hb == a.H) {
+        hb = 0;
+        ++bb;
+      }
     }
   }
 #pragma unroll
-  for (int w = 1; w < 8; w <<= 1) ss += __shfl_xor(ss, w);
-  float kmax = __builtin_sqrtf(ss), xmax = x;
+  for (int u = 0; u < kRecTiles; ++u) {
+    const float x = live[u] ? bias_value<KIND>(xb[u]) * a.mul : -INFINITY;
+    float ss = 0.f;
 #pragma unroll
-  for (int w = 8; w < 64; w <<= 1) {
-    kmax = fmaxf(kmax, __shfl_xor(kmax, w));
-    xmax = fmaxf(xmax, __shfl_xor(xmax, w));
+    for (int e = 0; e < 8; ++e) {
+      const float f = half_to_f32<F16>(kv[u][e]);
+      ss = __builtin_fmaf(f, f, ss);
+    }
+#pragma unroll
+    for (int w = 1; w < 8; w <<= 1) ss += __shfl_xor(ss, w);
+    float kmax = live[u] ? __builtin_sqrtf(ss) : 0.f, xmax = x;
+#pragma unroll
+    for (int w = 8; w < 64; w <<= 1) {
+      kmax = fmaxf(kmax, __shfl_xor(kmax, w));
+      xmax = fmaxf(xmax, __shfl_xor(xmax, w));
+    }
+    if (lane == 0) {
+      part[u][0][wave] = kmax;
+      part[u][1][wave] = xmax;
+    }
+    if (ch == 0 && tile0 + u < a.total) a.recs[(tile0 + u) * kRec + j] = x;
   }
-  if (lane == 0) {
-    part[0][wave] = kmax;
-    part[1][wave] = xmax;
-  }
-  float* rec = a.recs + tile * kRec;
-  if (ch == 0) rec[j] = x;
   __syncthreads();
-  if (tid < kRec - kKT) {
-    const float km = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
-    const float xm = fmaxf(fmaxf(part[1][0], part[1][1]), fmaxf(part[1][2], part[1][3]));
-    rec[kKT + tid] = tid == 0 ? a.c * km : tid == 1 ? a.c * xm : 0.f;
+  constexpr int kTail = kRec - kKT;                    // words after the 32 biases
+  if (tid < kRecTiles * kTail) {
+    const int u = tid / kTail, r = tid % kTail;
+    if (tile0 + u < a.total) {
+      const float km = fmaxf(fmaxf(part[u][0][0], part[u][0][1]), fmaxf(part[u][0][2], part[u][0][3]));
+      const float xm = fmaxf(fmaxf(part[u][1][0], part[u][1][1]), fmaxf(part[u][1][2], part[u][1][3]));
+      a.recs[(tile0 + u) * kRec + kKT + r] = r == 0 ? a.c * km : r == 1 ? a.c * xm : 0.f;
+    }
   }
 }
 
@@ -918,7 +954,6 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   ra.k = (const uint16_t*)k;
   ra.bias = bias;
   ra.recs = (float*)workspace;
-  ra.kind = bias_kind;
   ra.H = (int)H;
   ra.k_sb = k_sb; ra.k_sh = k_sh; ra.k_sn = k_sn;
   ra.sb = bias_sb; ra.sh = bias_sh; ra.sn = bias_sn;
@@ -930,8 +965,24 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   }
   ra.mul = 1.0f / sm_scale;
   ra.c = c;
-  hipLaunchKernelGGL(tile_records_kernel<F16>, dim3((unsigned)(B * H * ntiles)), dim3(256), 0, s,
-                     ra);
+  ra.total = B * H * ntiles;
+  {
+    const dim3 rgrid((unsigned)((ra.total + kRecTiles - 1) / kRecTiles)), rblock(256);
+    switch (bias_kind) {
+      case GPA_BIAS_F32:
+        hipLaunchKernelGGL((tile_records_kernel<F16, GPA_BIAS_F32>), rgrid, rblock, 0, s, ra);
+        break;
+      case GPA_BIAS_BF16:
+        hipLaunchKernelGGL((tile_records_kernel<F16, GPA_BIAS_BF16>), rgrid, rblock, 0, s, ra);
+        break;
+      case GPA_BIAS_F16:
+        hipLaunchKernelGGL((tile_records_kernel<F16, GPA_BIAS_F16>), rgrid, rblock, 0, s, ra);
+        break;
+      default:
+        hipLaunchKernelGGL((tile_records_kernel<F16, GPA_BIAS_NONE>), rgrid, rblock, 0, s, ra);
+        break;
+    }
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("%s: tile-record pre-pass launch failed: %s", fn,
