@@ -616,10 +616,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, hi = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bh = blockIdx.y;
+  // XCD-aware order: the hardware deals consecutive workgroups round-robin
+  // to the 8 XCDs, so each XCD is given a contiguous range of (batch-head,
+  // query block) items instead, and the query blocks of one batch-head share
+  // that XCD's L2 for their K and V (own-frame attention: 6 %).
+  int qb, bh;
+  {
+    const uint32_t T = gridDim.x * gridDim.y, L = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t q8 = T / 8, r8 = T % 8, x = L % 8;
+    const uint32_t item = x * q8 + (x < r8 ? x : r8) + L / 8;
+    qb = (int)(item % gridDim.x);
+    bh = (int)(item / gridDim.x);
+  }
   const int64_t b = bh / p.H, h = bh % p.H;
-  uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
-  const int64_t q_base = (int64_t)blockIdx.x * kQPerWG + wave * kQPerWave + l32;
+  uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + qb) * kWaves;
+  const int64_t q_base = (int64_t)qb * kQPerWG + wave * kQPerWave + l32;
   const float c = p.c;
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
@@ -931,6 +942,10 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
     return GPA_E_UNSUPPORTED;
   }
   const int64_t gx = (M + kQPerWG - 1) / kQPerWG;
+  if (gx * B * H > 0xffffffffLL) {   // the main pass numbers its workgroups in 32 bits
+    gpa_set_error("%s: %lld query blocks exceed the grid limit", fn, (long long)(gx * B * H));
+    return GPA_E_UNSUPPORTED;
+  }
   // Buffer offsets are 32-bit: one (batch, head) slice of K and V, plus the
   // tiles fetched past its end, must stay below 2^31 bytes.
   const int64_t span = N + (kMainAhead + 1) * kKT;
