@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|attn|merge|front|pool|sim16|attn16|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|attn|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   attn   biased attention, 16 heads x 274,800 queries x 68,700 keys x 64
@@ -10,6 +10,10 @@
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
   sim16  the similarity workload in fp16
   attn16 the attention workload in fp16
+  attn0  the attention workload with all-zero q, k, v (same shapes, bias and
+         code path): the instruction stream of `attn` with almost no
+         switching in the multipliers, to read the clock the power limit
+         allows against `attn` (GRBM_GUI_ACTIVE per dispatch; not in `all`)
   copy   a plain device copy of 1 GiB (bf16), the calibration for HBM byte
          counters: FETCH_SIZE / WRITE_SIZE of this dispatch should read
          1 GiB each, and the ratio to that is the counters' scale factor
@@ -34,7 +38,8 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "attn", "merge", "front", "pool", "sim16", "attn16", "copy", "all"):
+    if which not in ("sim", "attn", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
+                     "all"):
         print(__doc__, file=sys.stderr)
         return 2
 
@@ -108,6 +113,13 @@ def main(argv=None) -> int:
                 attention_keybias(q, k, v, b, 0.125)
             torch.cuda.synchronize()
             print(f"attn16 16x274800x68700x64 x {reps} done", flush=True)
+    if which == "attn0":
+        q, k, v, b = W.attn_inputs(device=dev)
+        q, k, v = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        for _ in range(reps):
+            attention_keybias(q, k, v, b, 0.125)
+        torch.cuda.synchronize()
+        print(f"attn0 16x274800x68700x64 (zero q, k, v) x {reps} done", flush=True)
     return 0
 
 
