@@ -168,6 +168,30 @@ def test_strided_views_from_fused_qkv(dev):
     _check(o, ref)
 
 
+@pytest.mark.parametrize("N", [45, 64, 7])
+def test_rows_past_n_never_reach_the_output(dev, N):
+    """k, v and the bias as views of the first N rows of larger buffers whose
+    other rows hold NaN.  The kernel fetches whole 32-key tiles and runs a
+    few tiles past the last one; those reads go through a buffer descriptor
+    that ends at the slice's last row and the tile offset is range-checked
+    with it, so they read zeros (and the records mask keys past N), and no
+    NaN reaches o or the LSE.  The loads stay inside the allocations."""
+    B, H, M = 1, 2, 300
+    q, k, v, b = _inputs(B, H, M, N, seed=N, bias="f32")
+    pad = 200
+    kb = torch.full((B, H, N + pad, 64), float("nan")).bfloat16()
+    vb = torch.full((B, H, N + pad, 64), float("nan")).bfloat16()
+    bb = torch.full((B, H, 1, N + pad), float("nan"))
+    kb[:, :, :N], vb[:, :, :N], bb[..., :N] = k, v, b
+    kd, vd, bd = kb.to(dev)[:, :, :N], vb.to(dev)[:, :, :N], bb.to(dev)[..., :N]
+    assert kd.stride(1) == (N + pad) * 64
+    o, lse = attention_keybias(q.to(dev), kd, vd, bd, 0.125, return_lse=True)
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    ref, ref_lse = attention_reference(q, k, v, b, 0.125)
+    _check(o, ref)
+    assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
+
+
 def test_fp32_inputs_follow_the_cast_contract(dev):
     q, k, v, b = _inputs(1, 2, 100, 130, seed=8, bias="f32")
     q32, k32, v32 = q.float().to(dev), k.float().to(dev), v.float().to(dev)

@@ -93,6 +93,26 @@ def test_strided_and_batched_inputs(dev):
     assert np.array_equal(vidx.cpu().numpy()[sure], fidx[sure])
 
 
+@pytest.mark.parametrize("M,N", [(300, 17), (300, 64), (2000, 1000), (3000, 9001)])
+def test_rows_past_n_never_win(dev, M, N):
+    """b as a view of the first N rows of a larger buffer whose other rows
+    would beat every real score (a constant vector of norm 90): the kernel
+    fetches 16-row tiles and stages past the end of each destination split,
+    and those rows must neither win nor move the maximum."""
+    a = _unit_bf16_values((1, M, 128), seed=M + N)
+    b = _unit_bf16_values((1, N, 128), seed=M + N + 1)
+    big = torch.full((1, N + 300, 128), 8.0)
+    big[:, :N] = b
+    db = big.bfloat16().to(dev)[:, :N]
+    vmax, vidx = fused_similarity_argmax(a.to(dev).bfloat16(), db)
+    vmax, vidx = vmax.float().cpu().numpy(), vidx.cpu().numpy()
+    assert vidx.max() < N
+    fmax, fidx, gap = sim_argmax_fp64(a, b)
+    assert np.abs(vmax - fmax).max() < 4e-3                          # bf16 output dtype
+    sure = gap > 1e-5
+    assert np.array_equal(vidx[sure], fidx[sure])
+
+
 def test_dtype_contract(dev):
     a = _unit_bf16_values((1, 64, 128), seed=3)
     b = _unit_bf16_values((1, 40, 128), seed=4)
