@@ -1,9 +1,11 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|attn|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|attn|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
+  sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
+         (not in `all`)
   attn   biased attention, 16 heads x 274,800 queries x 68,700 keys x 64
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
   front  merge front end: 274,800 fp32 metric rows of 1024 -> bf16 [dst | src] x 128
@@ -38,7 +40,7 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "attn", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
+    if which not in ("sim", "sim200", "attn", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
                      "all"):
         print(__doc__, file=sys.stderr)
         return 2
@@ -64,6 +66,13 @@ def main(argv=None) -> int:
             fused_similarity_argmax(s, d)
         torch.cuda.synchronize()
         print(f"sim 75000x25000x128 x {reps} done", flush=True)
+        del s, d
+    if which == "sim200":
+        s, d = W.sim_inputs(m=207_955, n=66_845, seed=1, device=dev)
+        for _ in range(reps):
+            fused_similarity_argmax(s, d)
+        torch.cuda.synchronize()
+        print(f"sim200 207955x66845x128 x {reps} done", flush=True)
         del s, d
     if which in ("merge", "all"):
         t, off, tok = W.merge_inputs(device=dev)
