@@ -23,11 +23,13 @@
 //
 // Work split: eight lanes own one (token, head, q|k) row, 16 bytes each;
 // the LayerNorm moments and the rotation partner (feature j <-> j+16 is lane
-// c <-> c^2 within the eight) are cross-lane exchanges.  A workgroup handles
-// 128 consecutive tokens of one (q|k, head), four rows per lane group, all
-// four loads issued before any arithmetic (one 16-byte load per lane in
-// flight held the kernel to ~3 TB/s); each pass of the group's 32 rows
-// writes one contiguous 4 KB (bf16) run.  HBM-bound.
+// c <-> c^2 within the eight) are cross-lane exchanges.  The 32 lane groups
+// of a workgroup own 32 consecutive (q|k, head) slices -- all of them at 16
+// heads -- of four consecutive tokens, so each pass reads 4 KB of
+// consecutive projection columns (one token's q and k), all four loads
+// issued before any arithmetic.  Reading 128-byte pieces of 6 KB-strided
+// rows instead (one head, many tokens per workgroup) ran 11 % slower; one
+// 16-byte load per lane in flight held the kernel to ~3 TB/s.  HBM-bound.
 #include "gpa_common.h"
 
 namespace gpa {
@@ -35,9 +37,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLanesPerRow = 8;
-constexpr int kRowsPerPass = kThreads / kLanesPerRow;   // 32
-constexpr int kPasses = 4;
-constexpr int kRowsPerBlock = kRowsPerPass * kPasses;
+constexpr int kSlicesPerBlock = kThreads / kLanesPerRow;   // 32 (q|k, head) slices
+constexpr int kTokens = 4;                                 // tokens per workgroup
 constexpr int kHeadDim = 64;
 
 struct QkArgs {
@@ -65,19 +66,28 @@ __device__ __forceinline__ float group_sum8(float v) {
 }
 
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
-  const int which = blockIdx.y & 1;            // 0: q, 1: k
-  const int64_t h = blockIdx.y >> 1;
+  // Lane group g owns slice 32*blockIdx.y + g (q heads, then k heads) for
+  // the kTokens tokens of blockIdx.x; groups past 2H load the last slice
+  // and store nothing.  Token numbers fit 32 bits (checked on the host),
+  // which keeps the index arithmetic off the 64-bit division path.
   const int c = threadIdx.x % kLanesPerRow;    // features 8c .. 8c+7
-  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
+  const uint32_t g = threadIdx.x / kLanesPerRow;
+  const uint32_t H = (uint32_t)a.H, N = (uint32_t)a.N;
+  const uint32_t slice = blockIdx.y * (uint32_t)kSlicesPerBlock + g;
+  const bool slice_ok = slice < 2 * H;
+  const uint32_t sl = slice_ok ? slice : 2 * H - 1;
+  const int which = sl < H ? 0 : 1;            // 0: q, 1: k
+  const uint32_t h = which ? sl - H : sl;
+  const int64_t col = (which ? a.k_offset : 0) + (int64_t)h * kHeadDim + c * 8;
+  const uint32_t tok0 = blockIdx.x * (uint32_t)kTokens;
+  const uint32_t last = (uint32_t)(a.rows - 1);
 
-  bf16x8 xv[kPasses];
+  bf16x8 xv[kTokens];
 #pragma unroll
-  for (int r = 0; r < kPasses; ++r) {
-    const int64_t row = row0 + r * kRowsPerPass;
-    const int64_t rc = row < a.rows ? row : a.rows - 1;   // every lane joins the exchanges
-    const int64_t b = rc / a.N, n = rc % a.N;
-    xv[r] = *reinterpret_cast<const bf16x8*>(a.qkv + b * a.sb + n * a.sn + which * a.k_offset +
-                                             h * kHeadDim + c * 8);
+  for (int r = 0; r < kTokens; ++r) {
+    const uint32_t row = min(tok0 + r, last);   // every lane joins the exchanges
+    const uint32_t b = row / N, n = row - b * N;
+    xv[r] = *reinterpret_cast<const bf16x8*>(a.qkv + (int64_t)b * a.sb + (int64_t)n * a.sn + col);
   }
   const float* w = a.w + which * kHeadDim + c * 8;
   const float* be = a.beta + which * kHeadDim + c * 8;
@@ -85,11 +95,10 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
   const bool out_f32 = which ? a.k_f32 : a.q_f32;
 
 #pragma unroll
-  for (int r = 0; r < kPasses; ++r) {
-    const int64_t row = row0 + r * kRowsPerPass;
-    const bool valid = row < a.rows;
-    const int64_t rc = valid ? row : a.rows - 1;
-    const int64_t b = rc / a.N, n = rc % a.N;
+  for (int r = 0; r < kTokens; ++r) {
+    const bool valid = slice_ok && tok0 + r <= last;
+    const uint32_t row = min(tok0 + r, last);
+    const uint32_t b = row / N, n = row - b * N;
     float x[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = (float)xv[r][i];
@@ -109,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
     for (int i = 0; i < 8; ++i) x[i] = x[i] * rstd * w[i] + be[i];
 
     if (a.pos != nullptr) {
-      int p = a.pos[(n % a.period) * 2 + (c >= 4 ? 1 : 0)];
+      int p = a.pos[(n % (uint32_t)a.period) * 2 + (c >= 4 ? 1 : 0)];
       p = p < 0 ? 0 : (p >= a.npos ? a.npos - 1 : p);
       const float sgn = (c & 2) ? 1.0f : -1.0f;   // second quarter of a half: +, first: -
       const float2* cs = reinterpret_cast<const float2*>(a.cs) + (int64_t)p * 16 + (c & 1) * 8;
@@ -124,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
     }
     if (!valid) continue;
 
-    const int64_t o = ((b * a.H + h) * a.N + n) * kHeadDim + c * 8;
+    const int64_t o = (((int64_t)b * H + h) * N + n) * kHeadDim + c * 8;
     if (out_f32) {
       f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(out) + o);
       dst[0] = f32x4{x[0], x[1], x[2], x[3]};
@@ -195,12 +204,13 @@ extern "C" int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int6
   a.q_out = q_out; a.k_out = k_out;
   a.q_f32 = q_dtype == GPA_DTYPE_F32; a.k_f32 = k_dtype == GPA_DTYPE_F32;
   a.B = B; a.N = N; a.H = H; a.rows = B * N;
-  const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (blocks > 0x7fffffff) {
+  const int64_t blocks = (a.rows + kTokens - 1) / kTokens;
+  const int64_t sblocks = (2 * H + kSlicesPerBlock - 1) / kSlicesPerBlock;
+  if (a.rows > 0xffffffffLL - kTokens || blocks > 0x7fffffff || period > 0x7fffffff) {
     gpa_set_error("gpa_qk_norm_rope_bf16: problem exceeds the grid limit");
     return GPA_E_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks, (unsigned)(2 * H)),
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks, (unsigned)sblocks),
                      dim3(kThreads), 0, (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -223,6 +223,34 @@ def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32):
     assert (q0.cpu().double() - y).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize("B,H,pad", [(2, 5, 64), (1, 24, 0), (3, 1, 8)])
+def test_qk_norm_rope_other_head_counts_and_strides(dev, B, H, pad):
+    """Any head count (the kernel walks (token, q|k head) items in projection
+    order, so a workgroup's items cross token rows whenever 2H is not 32),
+    B > 1, and projection rows wider than 3*H*64 (a view of a padded
+    tensor); against the fp64 textbook, fp32 outputs."""
+    g = torch.Generator(device=dev).manual_seed(B * 100 + H)
+    N = P + 37                      # not a multiple of the frame period
+    C = 3 * H * 64
+    wide = (torch.randn(B, N, C + pad, generator=g, device=dev) * 1.5 + 0.3).bfloat16()
+    qkv = wide[:, :, :C]
+    ln_w = 1 + 0.3 * torch.randn(2, 64, generator=g, device=dev)
+    ln_b = 0.2 * torch.randn(2, 64, generator=g, device=dev)
+    pos1 = A.frame_positions(GRID, PTS, dev)
+    rope = A.Rope2D(100.0).table(pos1, 64)
+    q, k = torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, rope.pos, rope.cs, H, True, True)
+    assert q.shape == (B, H, N, 64) and k.shape == (B, H, N, 64)
+    x = qkv.cpu().double().view(B, N, 3, H, 64).permute(2, 0, 3, 1, 4)
+    pos = pos1.cpu().repeat(2, 1)[:N]
+    for got, t, i in ((q, x[0], 0), (k, x[1], 1)):
+        mu = t.mean(-1, keepdim=True)
+        var = ((t - mu) ** 2).mean(-1, keepdim=True)
+        y = (t - mu) / torch.sqrt(var + 1e-5) * ln_w[i].cpu().double() + ln_b[i].cpu().double()
+        want = _rope_ref(y, pos).double()
+        err = (got.cpu().double() - want).abs()
+        assert (err <= 1e-5 * want.abs() + 1e-5).all(), f"max err {err.max().item():.3e}"
+
+
 def _pool_bf16_fp64(x: torch.Tensor, grid: int, kp: int):
     """fp64 scores of bf16-rounded normalised rows against bf16-rounded
     normalised seeds (the einsum of attention.py:130 under bf16 autocast,
