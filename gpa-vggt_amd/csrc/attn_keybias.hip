@@ -775,6 +775,40 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     }
   };
 
+  // A wave whose 64 queries all lie past M (waves 2 and 3 of the last query
+  // block of a batch-head when M mod 256 <= 128, e.g. 94 of 1,374) only
+  // carries its share of every tile's DMA: the same DMAs, waits and barriers
+  // as a live wave, no MFMA or softmax work, so the live wave sharing its
+  // SIMD gets the matrix pipe to itself.  Wave-uniform branch, taken before
+  // the live path starts.
+  if ((int64_t)qb * kQPerWG + wave * kQPerWave >= p.M) {
+#pragma unroll
+    for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+    wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
+    tile_barrier();
+    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    tile_barrier();
+    auto carry = [&](const int t, MainTile& Tissue) {
+      issue(t + kMainAhead, Tissue);
+      wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+      tile_barrier();
+    };
+    int t = 0;
+    for (; t + kMainSlots <= ntiles; t += kMainSlots) {
+#pragma unroll
+      for (int u = 0; u < kMainSlots; ++u) carry(t + u, *ring[(u + kMainAhead) % kMainSlots]);
+    }
+#pragma unroll
+    for (int u = 0; u < kMainSlots - 1; ++u)
+      if (t < ntiles) {
+        carry(t, *ring[(u + kMainAhead) % kMainSlots]);
+        ++t;
+      }
+    if (lane == 0) flag_row[wave] = 0;
+    wait_vm<0>();
+    return;
+  }
+
   // Prologue: tiles 0 .. kMainAhead-1 in flight; S(0) and the certification.
 #pragma unroll
   for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);

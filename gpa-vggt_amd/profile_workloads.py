@@ -1,12 +1,14 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|attn|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|attn|own|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
          (not in `all`)
   attn   biased attention, 16 heads x 274,800 queries x 68,700 keys x 64
+  own    own-frame attention of the frame-special split, 3,200 (frame, head)
+         pairs x 1,374 queries x 1,369 keys, no bias, with LSE (not in `all`)
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
   front  merge front end: 274,800 fp32 metric rows of 1024 -> bf16 [dst | src] x 128
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
@@ -40,7 +42,7 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "sim200", "attn", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
+    if which not in ("sim", "sim200", "attn", "own", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
                      "all"):
         print(__doc__, file=sys.stderr)
         return 2
@@ -122,6 +124,15 @@ def main(argv=None) -> int:
                 attention_keybias(q, k, v, b, 0.125)
             torch.cuda.synchronize()
             print(f"attn16 16x274800x68700x64 x {reps} done", flush=True)
+    if which == "own":
+        qf = (torch.randn(200, 16, 1374, 64, device=dev) / 8).bfloat16()
+        kf = (torch.randn(200, 16, 1369, 64, device=dev) / 8).bfloat16()
+        vf = (torch.randn(200, 16, 1369, 64, device=dev) / 8).bfloat16()
+        for _ in range(reps):
+            attention_keybias(qf, kf, vf, None, 0.125, return_lse=True)
+        torch.cuda.synchronize()
+        print(f"own 3200x1374x1369x64 x {reps} done", flush=True)
+        del qf, kf, vf
     if which == "attn0":
         q, k, v, b = W.attn_inputs(device=dev)
         q, k, v = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
