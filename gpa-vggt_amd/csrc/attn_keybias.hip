@@ -594,9 +594,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 // issues the record DMA (64 lanes x 16 bytes, so a slot's record area is
 // 1 KB, of which the first 144 bytes are the record): wave 0 into the slot,
 // the others into a scratch area nobody reads, so no wave-dependent branch
-// splits an iteration.  The unrolled iterations then form one basic block,
-// in which the pure arithmetic of an iteration could float down to its
-// consumers in the next one; an empty asm that takes the iteration's
+// splits an iteration; lanes outside the record read zeros by range.  The
+// unrolled iterations then form one basic block, in which the pure
+// arithmetic of an iteration could float down to its consumers in the next
+// one; an empty asm that takes the iteration's
 // results as operands keeps it inside.  250 VGPRs, two waves per SIMD.
 constexpr int kMainSlots = 5;
 constexpr int kMainAhead = kMainSlots - 1;  // tiles issued ahead of the one being softmaxed
@@ -665,7 +666,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const int s_key = slot >> 3, s_pc = slot & 7;
   const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
   const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
-  const uint32_t rec_voff = wave == 0 ? (uint32_t)lane * 16u : 0u;
+  // Only wave 0's first nine lanes fetch the 144-byte record; every other
+  // lane points past the descriptor's range (2^30 > any record row), so it
+  // lands zeros without touching memory.
+  const uint32_t rec_voff =
+      (wave == 0 && lane < (kRec * 4) / 16) ? (uint32_t)lane * 16u : 0x40000000u;
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
   auto issue = [&](int t, MainTile& T) {
     const uint32_t n0 = (uint32_t)t * kKT;
