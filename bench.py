@@ -192,7 +192,20 @@ def cpu_baseline(src, dst, q, k, v, bias, budget: float) -> dict:
                    f"({attn_rate / 1e12:.4f} TFLOP/s); per-step time extrapolated linearly "
                    f"(rows are independent)"),
         "host_cpus": os.cpu_count(),
+        "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "" where it is not readable."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
 
 
 def main(argv=None) -> int:
