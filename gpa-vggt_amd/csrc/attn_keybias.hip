@@ -153,6 +153,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);
 }
 
+// DMA of 4 bytes per lane into LDS at lds + 4*lane.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff,
+                                     uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+}
+
 // DMA of 16 bytes per lane into LDS at lds + 16*lane.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff,
                                       uint32_t soff) {
@@ -591,8 +598,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 //
 // Five ring slots keep tile t (V), tile t+1 (K, bias) and the three tiles
 // in flight; the DMA of tile t+4 refills the slot of tile t-1.  Every wave
-// issues the record DMA (64 lanes x 16 bytes, so a slot's record area is
-// 1 KB, of which the first 144 bytes are the record): wave 0 into the slot,
+// issues the record DMA (64 lanes x 4 bytes, so a slot's record area is
+// 256 bytes, of which the first 144 are the record): wave 0 into the slot,
 // the others into a scratch area nobody reads, so no wave-dependent branch
 // splits an iteration; lanes outside the record read zeros by range.  The
 // unrolled iterations then form one basic block, in which the pure
@@ -605,13 +612,13 @@ constexpr int kMainAhead = kMainSlots - 1;  // tiles issued ahead of the one bei
 struct alignas(16) MainTile {
   uint16_t k[kKT * kHD];
   uint16_t v[kKT * kHD];
-  float rec[256];
+  float rec[64];
 };
 
 template <bool F16>
 __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   __shared__ MainTile ring0, ring1, ring2, ring3, ring4;
-  __shared__ float rec_sink[256];
+  __shared__ float rec_sink[64];
   MainTile* const ring[kMainSlots] = {&ring0, &ring1, &ring2, &ring3, &ring4};
 
   const int tid = threadIdx.x;
@@ -666,18 +673,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const int s_key = slot >> 3, s_pc = slot & 7;
   const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
   const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
-  // Only wave 0's first nine lanes fetch the 144-byte record; every other
-  // lane points past the descriptor's range (2^30 > any record row), so it
-  // lands zeros without touching memory.
-  const uint32_t rec_voff =
-      (wave == 0 && lane < (kRec * 4) / 16) ? (uint32_t)lane * 16u : 0x40000000u;
+  // The record DMA moves 4 bytes per lane: wave 0's first 36 lanes fetch the
+  // 144-byte record; every other lane points past the descriptor's range
+  // (2^30 > any record row), so it lands zeros without touching memory.
+  const uint32_t rec_voff = (wave == 0 && lane < kRec) ? (uint32_t)lane * 4u : 0x40000000u;
   const int ntiles = (int)((p.N + kKT - 1) / kKT);
   auto issue = [&](int t, MainTile& T) {
     const uint32_t n0 = (uint32_t)t * kKT;
     dma16(krs, &T.k[wave * 512], k_voff, n0 * k_row);
     dma16(vrs, &T.v[wave * 512], v_voff, n0 * v_row);
     float* dst = wave == 0 ? &T.rec[0] : &rec_sink[0];   // wave-uniform M0, no branch
-    dma16(rrs, dst, rec_voff, (uint32_t)t * (kRec * 4));
+    dma4(rrs, dst, rec_voff, (uint32_t)t * (kRec * 4));
   };
   // A tile has landed once at most the DMAs of the NT tiles issued after it
   // (three instructions per tile) are outstanding.
