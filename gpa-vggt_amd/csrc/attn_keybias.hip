@@ -758,13 +758,30 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     bf16x8 pb[2];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
+      // Source order steers the compiler here.  fp16: the eight exp2 first,
+      // then the packs, or most packs sit right after their exp2 and take a
+      // wait state each (90 s_nop per five iterations against 23).  bf16:
+      // pairwise, or the packs get split into single conversions and perms.
+      if constexpr (F16) {
+        float pe[8];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
-        const bf16x2 pv2 = pack2<F16>(p0, p1);
-        pb[half][e] = pv2[0];
-        pb[half][e + 1] = pv2[1];
+        for (int e = 0; e < 8; ++e)
+          pe[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const bf16x2 pv2 = pack2<F16>(pe[e], pe[e + 1]);
+          pb[half][e] = pv2[0];
+          pb[half][e + 1] = pv2[1];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e], c, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 * half + e + 1], c, neg_m));
+          const bf16x2 pv2 = pack2<F16>(p0, p1);
+          pb[half][e] = pv2[0];
+          pb[half][e + 1] = pv2[1];
+        }
       }
       const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
       const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
