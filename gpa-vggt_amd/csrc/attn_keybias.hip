@@ -604,8 +604,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 // splits an iteration; lanes outside the record read zeros by range.  The
 // unrolled iterations then form one basic block, in which the pure
 // arithmetic of an iteration could float down to its consumers in the next
-// one; an empty asm that takes the iteration's
-// results as operands keeps it inside.  250 VGPRs, two waves per SIMD.
+// one; an empty asm that takes the iteration's results as operands keeps it
+// inside.  250 VGPRs, two waves per SIMD.
 constexpr int kMainSlots = 5;
 constexpr int kMainAhead = kMainSlots - 1;  // tiles issued ahead of the one being softmaxed
 
