@@ -72,6 +72,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace gpa {
@@ -1139,4 +1140,80 @@ extern "C" int gpa_attn_keybias_f16(const void* q, const void* k, const void* v,
                                 bias_sh, bias_sn, o, lse, B, H, M, N, D, q_sb, q_sh, q_sm, k_sb,
                                 k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sm, lse_sb, lse_sh,
                                 workspace, workspace_bytes, sm_scale, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The allocation-free variant: the workspace is a device-resident array of
+// this file.  Each GPU the library runs on holds its own copy (allocated by
+// the runtime with the code object, kept until the process ends).  Host code
+// never passes the array's name to a kernel: on the host that name is a
+// stand-in, not a device address.  The device address is resolved once per
+// device with hipGetSymbolAddress, on that device's first call, and every
+// later use goes through the resolved pointer.
+//
+// The pre-passes and the main pass write every workspace byte a call reads
+// (tile records, row bounds, one flag per wave) before reading it, so nothing
+// has to be cleared between calls.  Calls that overlap on one GPU (two host
+// threads, or two streams) share the array and race.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[GPA_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of this GPU's `scratch` (the current device's), or nullptr
+// with the error message set.
+void* scratch_for_current_device(const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    gpa_set_error("%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    gpa_set_error("%s: device %d is beyond the %d devices the scratch table holds", fn, dev,
+                  kMaxScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      gpa_set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                    hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int gpa_attn_keybias_bf16_noalloc(
+    const void* q, const void* k, const void* v, const void* bias, int bias_kind,
+    int64_t bias_sb, int64_t bias_sh, int64_t bias_sn, void* o, float* lse, int64_t B, int64_t H,
+    int64_t M, int64_t N, int64_t D, int64_t q_sb, int64_t q_sh, int64_t q_sm, int64_t k_sb,
+    int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
+    int64_t o_sh, int64_t o_sm, int64_t lse_sb, int64_t lse_sh, float sm_scale, void* stream) {
+  static const char* fn = "gpa_attn_keybias_bf16_noalloc";
+  gpa_clear_error();
+  if (B > 0 && H > 0 && M > 0 && N > 0) {
+    const size_t need = attn_ws_bytes(B, H, M, N);
+    if (need > (size_t)GPA_ATTN_NOALLOC_SCRATCH_BYTES) {
+      gpa_set_error("%s: this shape needs %zu bytes of workspace, the static scratch holds %zu "
+                    "(use gpa_attn_keybias_bf16 with a caller workspace)",
+                    fn, need, (size_t)GPA_ATTN_NOALLOC_SCRATCH_BYTES);
+      return GPA_E_UNSUPPORTED;
+    }
+  }
+  void* ws = scratch_for_current_device(fn);
+  if (!ws) return GPA_E_LAUNCH;
+  return attn_keybias_run<false>(fn, q, k, v, bias, bias_kind, bias_sb, bias_sh, bias_sn, o, lse,
+                                 B, H, M, N, D, q_sb, q_sh, q_sm, k_sb, k_sh, k_sn, v_sb, v_sh,
+                                 v_sn, o_sb, o_sh, o_sm, lse_sb, lse_sh, ws,
+                                 (size_t)GPA_ATTN_NOALLOC_SCRATCH_BYTES, sm_scale, stream);
 }

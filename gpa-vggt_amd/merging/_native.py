@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -45,6 +45,10 @@ GPA_BIAS_NONE = 0
 GPA_BIAS_F32 = 1
 GPA_BIAS_BF16 = 2
 GPA_BIAS_F16 = 3
+
+# Bytes of the static device scratch behind gpa_attn_keybias_bf16_noalloc
+# (GPA_ATTN_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 GPA_DTYPE_F32 = 0
 GPA_DTYPE_BF16 = 1
@@ -99,6 +103,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     ]
     lib.gpa_attn_keybias_f16.restype = ctypes.c_int
     lib.gpa_attn_keybias_f16.argtypes = lib.gpa_attn_keybias_bf16.argtypes
+    lib.gpa_attn_keybias_bf16_noalloc.restype = ctypes.c_int
+    lib.gpa_attn_keybias_bf16_noalloc.argtypes = (
+        lib.gpa_attn_keybias_bf16.argtypes[:-4] + [ctypes.c_float, _vp])   # no workspace
     lib.gpa_lse_combine_bf16.restype = ctypes.c_int
     lib.gpa_lse_combine_bf16.argtypes = [_vp] * 5 + [_i64] * 5 + [_i64] * 16 + [_i64] * 3 + [_vp]
     lib.gpa_qk_norm_rope_bf16.restype = ctypes.c_int
@@ -168,7 +175,8 @@ def exported_symbols() -> Tuple[str, ...]:
             "gpa_sim_argmax_bf16", "gpa_attn_keybias_workspace_bytes", "gpa_attn_keybias_bf16",
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
             "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
-            "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16")
+            "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16",
+            "gpa_attn_keybias_bf16_noalloc")
 
 
 def _check(rc: int, what: str) -> None:

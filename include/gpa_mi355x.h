@@ -1,8 +1,8 @@
 /*
  * gpa_mi355x.h — C ABI of the MI355X (gfx950) GPA-VGGT merging hot path.
  *
- * Eight entry points (two of them with an fp16 twin) sit behind this
- * boundary:
+ * Eight entry points (two of them with an fp16 twin, the attention also
+ * with an allocation-free variant) sit behind this boundary:
  *
  *   gpa_sim_argmax_bf16   — fused cosine-similarity row max / argmax between
  *                           source and destination token metrics
@@ -29,14 +29,17 @@
  *
  * Conventions shared by every entry point:
  *   - All tensor pointers are device pointers owned by the caller.  The
- *     library allocates nothing and keeps no reference after returning.
+ *     library allocates nothing and keeps no reference after returning
+ *     (gpa_attn_keybias_bf16_noalloc uses the library's one static device
+ *     array instead of a caller workspace).
  *   - Element strides are in elements (not bytes).  The innermost (feature)
  *     dimension has unit stride; row pointers must be 16-byte aligned.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
  *     legacy default stream).  Functions return GPA_OK (0) after a successful
  *     launch or a negative GPA_E* code; gpa_last_error() then holds a
  *     message for the calling thread.
- *   - The library is stateless and reentrant: tile shapes are a deterministic
+ *   - The library is stateless and reentrant (except for the shared scratch
+ *     of gpa_attn_keybias_bf16_noalloc): tile shapes are a deterministic
  *     function of the problem shape (no autotuning, no global caches).
  */
 #ifndef GPA_MI355X_H
@@ -49,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 8
+#define GPA_ABI_VERSION 9
 
 enum {
   GPA_OK = 0,
@@ -161,6 +164,35 @@ int gpa_attn_keybias_f16(const void* q, const void* k, const void* v,
                          int64_t lse_sb, int64_t lse_sh,
                          void* workspace, size_t workspace_bytes,
                          float sm_scale, void* stream);
+
+/* Bytes of the device-resident scratch array behind
+ * gpa_attn_keybias_bf16_noalloc (one per GPU, held until the process ends). */
+#define GPA_ATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * gpa_attn_keybias_bf16 without the workspace arguments: the workspace is a
+ * static device array of GPA_ATTN_NOALLOC_SCRATCH_BYTES in the library, so
+ * the call allocates nothing (no hipMalloc/hipFree, no allocating library
+ * routine).  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  Same arguments, semantics and kernels otherwise.
+ * Shapes whose gpa_attn_keybias_workspace_bytes(B, H, M, N) exceeds the
+ * array are refused with GPA_E_UNSUPPORTED.  The array is resolved on the
+ * current device at its first call there; `stream` must belong to the
+ * current device.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other threads, other streams) race.
+ */
+int gpa_attn_keybias_bf16_noalloc(const void* q, const void* k, const void* v,
+                                  const void* bias, int bias_kind,
+                                  int64_t bias_sb, int64_t bias_sh, int64_t bias_sn,
+                                  void* o, float* lse,
+                                  int64_t B, int64_t H, int64_t M, int64_t N, int64_t D,
+                                  int64_t q_sb, int64_t q_sh, int64_t q_sm,
+                                  int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                  int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                  int64_t o_sb, int64_t o_sh, int64_t o_sm,
+                                  int64_t lse_sb, int64_t lse_sh,
+                                  float sm_scale, void* stream);
 
 /*
  * Deterministic segmented reduction of token rows: the K/V merge.

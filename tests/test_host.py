@@ -118,6 +118,26 @@ def test_attn_empty_problem_is_a_no_op():
     assert _attn(M=0) == _native.GPA_OK
 
 
+def test_attn_noalloc_refuses_shapes_beyond_the_scratch():
+    """The size check of the allocation-free entry point comes before any
+    HIP call, so it is a host test: 64 heads x 2^20 keys need ~300 MB of
+    tile records, more than the static scratch holds."""
+    lib = _native.lib()
+    B, H, M, N = 1, 64, 256, 1 << 20
+    assert lib.gpa_attn_keybias_workspace_bytes(B, H, M, N) > _native.NOALLOC_SCRATCH_BYTES
+    rc = lib.gpa_attn_keybias_bf16_noalloc(
+        FAKE, FAKE, FAKE, None, 0, 0, 0, 0, FAKE, None, B, H, M, N, 64,
+        0, M * 64, 64, 0, N * 64, 64, 0, N * 64, 64, 0, M * 64, 64, 0, 0, 0.125, None)
+    assert rc == _native.GPA_E_UNSUPPORTED
+    assert b"static scratch" in lib.gpa_last_error()
+    # the largest 200-frame workloads fit: 16 heads x 219,840 keys (core
+    # blocks) and the own-frame call (3,200 batch-heads x 1,369 keys)
+    assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 274_800, 219_840) <= \
+        _native.NOALLOC_SCRATCH_BYTES
+    assert lib.gpa_attn_keybias_workspace_bytes(200, 16, 1374, 1369) <= \
+        _native.NOALLOC_SCRATCH_BYTES
+
+
 def test_attn_workspace_bytes():
     lib = _native.lib()
     # per (batch, head): one 144-byte record per 32-key tile, 8 bytes of row
