@@ -199,6 +199,9 @@ class GpaAttention(nn.Module):
         self.frame_special = False
         self.merge_ratio = cfg.merge_ratio
         self.tracer: Optional["StageTimer"] = None
+        # When a list: every merge / pooling of this module appends a record
+        # (device tensors, no host synchronisation inside the forward).
+        self.merge_log: Optional[list] = None
 
     def _mark(self, name: str) -> None:
         if self.tracer is not None:
@@ -254,6 +257,11 @@ class GpaAttention(nn.Module):
                                         num_special=self.cfg.num_special)
             k = m.heads(k, "mean")
             v = m.heads(v, "mean")
+            if self.merge_log is not None:
+                self.merge_log.append({"kind": "merged", "block": global_merging, "tokens": N,
+                                       "num_dst": m.index.num_dst, "r": m.index.r,
+                                       "size": m.size, "slot_offsets": m.index.slot_offsets,
+                                       "keys": k.shape[2]})
             bias = m.size.reshape(B, 1, 1, -1).log().to(q.dtype).expand(B, H, 1, k.shape[2])
             self._mark("merge")
             out = attention_keybias(q, k, v, bias, self.scale)
@@ -288,6 +296,8 @@ class GpaAttention(nn.Module):
         if kp > 0:
             pooled_k, pooled_v, pool_size, _ = torch.ops.gpa.pool_shared(
                 k, v, S, pts, g, kp, False)
+            if self.merge_log is not None:
+                self.merge_log.append({"kind": "pool", "frames": S, "pool_size": pool_size})
             sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
             sh_v = torch.cat([v5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_v], dim=2)
             bias = torch.zeros(B, H, 1, sh_k.shape[2], device=q.device, dtype=torch.float32)
@@ -463,6 +473,12 @@ class GpaAggregator(nn.Module):
         self.tracer = tracer
         for blk in list(self.frame_blocks) + list(self.global_blocks):
             blk.attn.tracer = tracer
+
+    def set_merge_log(self, log: Optional[list]) -> None:
+        """Collect one record per merge and per shared-set pooling of the
+        global blocks into `log` (None stops collecting)."""
+        for blk in self.global_blocks:
+            blk.attn.merge_log = log
 
     def _mark(self, name: str) -> None:
         if self.tracer is not None:

@@ -11,7 +11,11 @@ Orderings the reference leaves to torch's sort are fixed here:
     each class -- a stable sort of the -1/0 mask;
   * merge order (reference :199): descending node_max, ties by increasing
     source position -- a stable descending sort.
-These are the orders torch's GPU radix sort produces for such inputs.
+On the GPU the reference's own calls (`reshape(1, -1, 1).argsort(dim=1)`
+and `argsort(dim=-1, descending=True)`, torch's default sort) give exactly
+these orders, for masks of 1 to 200 frames and node_max rows of 1,045 to
+207,955 entries with tied values (tests/test_gpu_sort_order.py), so the
+stable sorts change no result while making the order a documented property.
 `merge.index` exposes the index tensors for inspection.
 
 Under bf16 or fp16 autocast (the model's and the evaluation stack's

@@ -21,7 +21,7 @@ import torch
 import gpa_workloads as W
 from merging import _native
 from merging.merge import _projection, dst_mask, num_dst_tokens, token_merge_bipartite2d
-from oracle.similarity import bf16_top2_gap
+from oracle.similarity import bf16_top2_gap, fast_similarity_chunks
 
 pytestmark = pytest.mark.gpu
 
@@ -148,8 +148,9 @@ def test_zero_row_gives_nan_like_the_reference(dev):
 
 def test_token_merge_uses_the_front_end_under_autocast(dev):
     """The merge under autocast: node_max stays fp32 (the reference's division
-    promotes to fp32), and the node indices agree with the similarity of the
-    torch chain's operands under the top-2 gap rule."""
+    promotes to fp32), and the node indices agree with the oracle's chunked
+    bf16 similarity (merging/merge.py:13-36, on the CPU) of the torch
+    chain's operands under the top-2 gap rule."""
     frames, ns = 4, 5
     metric = W.shifted_basis_tokens(frames, seed=5).to(dev)
     n = metric.shape[1]
@@ -164,10 +165,12 @@ def test_token_merge_uses_the_front_end_under_autocast(dev):
     order = torch.cat([ix.b_idx, ix.a_idx])
     ab = _torch_chain(metric, _projection(dev, 1024, 128, torch.float32), order, True)
     a, b = ab[:, num_dst:], ab[:, :num_dst]
-    ref_max, ref_idx = torch.ops.gpa.sim_argmax(a, b)
-    keep = (bf16_top2_gap(a, b) >= 1e-3).to(dev)
-    assert torch.equal(ix.node_idx[keep], ref_idx[keep])
-    assert (ix.node_max - ref_max).abs().max().item() < 2e-2
+    ref_max, ref_idx = fast_similarity_chunks(a.cpu(), b.cpu().transpose(1, 2), 5000)
+    keep = (bf16_top2_gap(a, b) >= 1e-3).cpu()
+    assert keep.float().mean() > 0.5
+    assert torch.equal(ix.node_idx.cpu()[keep], ref_idx[keep])
+    # the oracle's max is the bf16-rounded score, the kernel's the fp32 one
+    assert (ix.node_max.cpu() - ref_max.float()).abs().max().item() <= 2.0 ** -8
     assert m.size.sum().item() == n
 
 
@@ -203,6 +206,7 @@ def test_token_merge_under_fp16_autocast(dev):
     ab = _torch_chain(metric, _projection(dev, 1024, 128, torch.float32), order, True,
                       torch.float16)
     a, b = ab[:, num_dst:], ab[:, :num_dst]
-    _, ref_idx = torch.ops.gpa.sim_argmax(a, b)
-    keep = (bf16_top2_gap(a, b) >= 1e-3).to(dev)
-    assert torch.equal(ix.node_idx[keep], ref_idx[keep])
+    _, ref_idx = fast_similarity_chunks(a.cpu(), b.cpu().transpose(1, 2), 5000)
+    keep = (bf16_top2_gap(a, b) >= 1e-3).cpu()
+    assert keep.float().mean() > 0.5
+    assert torch.equal(ix.node_idx.cpu()[keep], ref_idx[keep])
