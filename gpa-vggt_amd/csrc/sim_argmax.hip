@@ -23,6 +23,9 @@
 //     all workgroups on one XCD read the same destination range and that
 //     range stays resident in the XCD's L2.  Partial (max, idx) pairs per
 //     split are merged by a second tiny kernel with the same tie rule.
+//   * Above D = 256 (the unprojected 1024-d metric) source rows no longer fit
+//     in VGPRs; sim_argmax_gemm_kernel tiles 128 x 128 with both operands in
+//     LDS and loops over the features (see there).
 #include "gpa_common.h"
 
 #include <math.h>
@@ -478,6 +481,226 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
   }
 }
 
+// D > 256 (the unprojected metric, D = 1024 for VGGT-1B): source rows no
+// longer fit in VGPRs, so both operands stream through LDS, GEMM-style.
+//   * A workgroup tile is 128 source x 128 destination rows; wave w owns the
+//     64 x 64 quadrant (source half w & 1, destination half w >> 1) as 4 x 4
+//     accumulators of v_mfma_f32_16x16x32 (S^T = Dst . Src^T, so a lane again
+//     holds one source row against 4 destination rows per block).
+//   * The feature dimension is walked in stages of 32 (one MFMA k-step):
+//     8 KB of source and 8 KB of destination rows per stage, filled by
+//     buffer_load ... lds DMA (four instructions per wave) into a ring of
+//     four stages, three in flight while one is computed; one barrier per
+//     stage.  Rows are 64 bytes with their four 16-byte chunks swizzled by
+//     (row >> 2) & 3, so the 16 lanes reading one chunk of 16 rows hit 16
+//     distinct bank groups.
+//   * After the last stage of a destination tile the 64 scores per lane fold
+//     into the lane's running (max, index) per source block, in increasing
+//     destination order with a strict `>` (earlier index kept on ties), and
+//     the accumulators restart from zero.  Destination rows past the split
+//     read zeros and are masked in the fold; source rows past M read zeros
+//     and are not stored.
+//   * The stage sequence runs over (destination tile, feature chunk) pairs
+//     without a break, so the ring keeps streaming across tile boundaries.
+//   * At the end the four lanes of a source row reduce with the lowest-index
+//     rule, and the two destination halves meet in LDS.
+constexpr int kGT = 128;                 // source and destination rows per tile
+constexpr int kGStage = kGT * 32 * 2;    // bytes of one operand per 32-feature stage
+constexpr int kGRing = 4;
+
+template <bool F16>
+__global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int D) {
+  __shared__ __attribute__((aligned(16))) uint8_t a0[kGStage], a1[kGStage], a2[kGStage],
+      a3[kGStage], b0[kGStage], b1[kGStage], b2[kGStage], b3[kGStage];
+  __shared__ float x_best[kGT];
+  __shared__ int x_idx[kGT];
+  uint8_t* const ra[kGRing] = {a0, a1, a2, a3};
+  uint8_t* const rb[kGRing] = {b0, b1, b2, b3};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int quad = lane >> 4, l16 = lane & 15;
+  const int64_t batch = blockIdx.y;
+  int mblock, split;
+  map_block(p, blockIdx.x, mblock, split);
+  mblock = __builtin_amdgcn_readfirstlane(mblock);
+  split = __builtin_amdgcn_readfirstlane(split);
+  const int64_t m_wg = (int64_t)mblock * kGT;
+  if (m_wg >= p.M) return;  // padding block: the whole workgroup leaves together
+
+  const int64_t n_begin = (int64_t)split * p.n_chunk;
+  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
+  const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + kGT - 1) / kGT) : 0;
+  const int nk = D / 32;
+  const int nstages = ntiles * nk;
+
+  // Range-checked descriptors: source rows [m_wg, M) of this workgroup and
+  // destination rows [n_begin, n_end) of this split; anything past reads 0.
+  const int64_t m_rows = min((int64_t)kGT, p.M - m_wg);
+  const uint32_t a_row = (uint32_t)p.a_sm * 2u, b_row = (uint32_t)p.b_sn * 2u;
+  const __amdgpu_buffer_rsrc_t ars = make_rsrc(p.a + batch * p.a_sb + m_wg * p.a_sm,
+                                               (uint32_t)(((m_rows - 1) * p.a_sm + D) * 2));
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(
+      p.b + batch * p.b_sb + n_begin * p.b_sn,
+      n_end > n_begin ? (uint32_t)(((n_end - n_begin - 1) * p.b_sn + D) * 2) : 0u);
+  // DMA roles: instruction j of wave w fills rows 32w + 16j .. +16 of a stage;
+  // lane l lands at row +l/4, chunk l%4 and fetches the logical chunk the
+  // swizzle puts there.
+  uint32_t a_voff[2], b_voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = wave * 32 + j * 16 + (lane >> 2);
+    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    a_voff[j] = (uint32_t)row * a_row + ch * 16;
+    b_voff[j] = (uint32_t)row * b_row + ch * 16;
+  }
+  auto issue = [&](int s, uint8_t* A, uint8_t* Bd) {
+    const int t = s / nk, kc = s - t * nk;
+    const uint32_t ks = (uint32_t)kc * 64u;
+    const uint32_t ts = (uint32_t)t * kGT * b_row + ks;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ars, (__attribute__((address_space(3))) void*)(A + (wave * 32 + j * 16) * 64), 16,
+          a_voff[j], ks, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          brs, (__attribute__((address_space(3))) void*)(Bd + (wave * 32 + j * 16) * 64), 16,
+          b_voff[j], ts, 0, 0);
+    }
+  };
+  // Fragment reads: row l16 of a 16-row block, logical chunk `quad`.
+  int s_off[4], d_off[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int rs = wm * 64 + blk * 16 + l16, rd = wn * 64 + blk * 16 + l16;
+    s_off[blk] = rs * 64 + ((quad ^ ((rs >> 2) & 3)) << 4);
+    d_off[blk] = rd * 64 + ((quad ^ ((rd >> 2) & 3)) << 4);
+  }
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
+  float best[4];
+  int bidx[4];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb) {
+    best[sb] = -INFINITY;
+    bidx[sb] = (int)n_begin;
+  }
+
+  auto compute = [&](const uint8_t* A, const uint8_t* Bd) {
+    bf16x8 sf[4], df[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      sf[blk] = *reinterpret_cast<const bf16x8*>(A + s_off[blk]);
+      df[blk] = *reinterpret_cast<const bf16x8*>(Bd + d_off[blk]);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[sb][db] = mfma16x16x32_t<F16>(df[db], sf[sb], acc[sb][db]);
+  };
+  // Fold the finished scores of destination tile t, then restart the sums.
+  auto fold = [&](int t) {
+    const int64_t base = n_begin + (int64_t)t * kGT + wn * 64 + 4 * quad;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t n = base + db * 16 + r;
+          const float v = acc[sb][db][r];
+          const bool upd = v > best[sb] && n < n_end;
+          best[sb] = upd ? v : best[sb];
+          bidx[sb] = upd ? (int)n : bidx[sb];
+        }
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
+  };
+
+  // Stage s: wait until it has landed (the DMAs of the stages issued after
+  // it may stay in flight), synchronise, refill the slot stage s-1 used with
+  // stage s+3, compute, and fold at the end of a destination tile.
+  auto step = [&](int s, const int u) {
+    wait_vm<4 * (kGRing - 2)>();    // the two stages issued after s may stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Unconditional: the last stages fetch a destination tile past the
+    // split, which the descriptor turns into zeros (a branch here would make
+    // the compiler drain every DMA before the next LDS read).
+    issue(s + kGRing - 1, ra[(u + kGRing - 1) % kGRing], rb[(u + kGRing - 1) % kGRing]);
+    compute(ra[u], rb[u]);
+    const int t = s / nk;
+    if (s - t * nk == nk - 1) fold(t);
+  };
+
+#pragma unroll
+  for (int i = 0; i < kGRing - 1; ++i) issue(i, ra[i], rb[i]);
+  int s = 0;
+  for (; s + kGRing <= nstages; s += kGRing) {
+#pragma unroll
+    for (int u = 0; u < kGRing; ++u) step(s + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u < kGRing - 1; ++u)
+    if (s < nstages) step(s++, u);
+  wait_vm<0>();
+
+  // Four lanes per source row (quads), lowest index on ties.
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb) {
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float ov = __shfl_xor(best[sb], sh);
+      const int oi = __shfl_xor(bidx[sb], sh);
+      if (ov > best[sb] || (ov == best[sb] && oi < bidx[sb])) {
+        best[sb] = ov;
+        bidx[sb] = oi;
+      }
+    }
+  }
+  // The second destination half hands its results to the first over LDS.
+  if (wn == 1 && quad == 0) {
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      x_best[wm * 64 + sb * 16 + l16] = best[sb];
+      x_idx[wm * 64 + sb * 16 + l16] = bidx[sb];
+    }
+  }
+  __syncthreads();
+  if (wn == 0 && quad == 0) {
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      const int r = wm * 64 + sb * 16 + l16;
+      float bv = best[sb];
+      int bi = bidx[sb];
+      const float ov = x_best[r];
+      const int oi = x_idx[r];
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+      const int64_t m = m_wg + r;
+      if (m < p.M) {
+        if (p.splits == 1) {
+          p.out_max[batch * p.omax_sb + m] = bv;
+          p.out_idx[batch * p.oidx_sb + m] = bi;
+        } else {
+          const int64_t o = (batch * p.splits + split) * p.M + m;
+          p.part_max[o] = bv;
+          p.part_idx[o] = bi;
+        }
+      }
+    }
+  }
+}
+
 // Merge per-split partials in split order; strict `>` keeps the earlier
 // split (lower destination indices) on ties.
 __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_t B) {
@@ -505,9 +728,13 @@ struct SimPlan {
   size_t ws_bytes;
 };
 
+// Largest feature dim of the GEMM-tiled kernel (D > 256).
+constexpr int64_t kMaxD = 4096;
+
 SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   SimPlan pl{};
-  const int rows = rows_per_wg((int)(D / 32));
+  const bool gemm = D > 256;
+  const int rows = gemm ? kGT : rows_per_wg((int)(D / 32));
   const int64_t mb = (M + rows - 1) / rows;
   // Split the destination range until the grid holds >= 2048 workgroups
   // (8 per CU on 256 CUs) or a split would drop below 512 rows.  Once there
@@ -523,7 +750,8 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   }
   pl.mblocks = (int)mbp;
   const int64_t per = (N + splits - 1) / splits;
-  pl.n_chunk = (per + kTN - 1) / kTN * kTN;
+  const int gran = gemm ? kGT : kTN;      // whole destination tiles per split
+  pl.n_chunk = (per + gran - 1) / gran * gran;
   pl.ws_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
   return pl;
 }
@@ -562,9 +790,9 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
     gpa_set_error("%s: null tensor pointer", fn);
     return GPA_E_INVALID;
   }
-  if (D % 32 != 0 || D < 32 || D > 256) {
-    gpa_set_error("%s: feature dim D=%lld unsupported (multiple of 32, 32..256)", fn,
-                  (long long)D);
+  if (D % 32 != 0 || D < 32 || D > kMaxD) {
+    gpa_set_error("%s: feature dim D=%lld unsupported (multiple of 32, 32..%lld)", fn,
+                  (long long)D, (long long)kMaxD);
     return GPA_E_UNSUPPORTED;
   }
   if (N > (int64_t)0x7fffff00 || M > ((int64_t)1 << 40)) {
@@ -588,9 +816,10 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
   // Buffer offsets are 32-bit: one split of destination rows, plus the
   // tiles fetched past its end (two stages, or eight 16-row tiles), must
   // stay below 2^31 bytes.
-  if ((pl.n_chunk + 2 * kTN) * b_sn * 2 >= ((int64_t)1 << 31)) {
-    gpa_set_error("%s: destination split exceeds 2 GiB (N=%lld, row stride %lld)", fn,
-                  (long long)N, (long long)b_sn);
+  if ((pl.n_chunk + 2 * kTN) * b_sn * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)kGT * a_sm * 2 >= ((int64_t)1 << 31)) {
+    gpa_set_error("%s: destination split or source block exceeds 2 GiB (N=%lld, row strides "
+                  "%lld / %lld)", fn, (long long)N, (long long)a_sm, (long long)b_sn);
     return GPA_E_UNSUPPORTED;
   }
   SimArgs p{};
@@ -633,8 +862,8 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      gpa_set_error("%s: D=%lld has no kernel instance", fn, (long long)D);
-      return GPA_E_UNSUPPORTED;
+      hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
+      break;
   }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && pl.splits > 1) {

@@ -6,6 +6,8 @@ name, arguments, dtype contract and return types
 hand-written HIP kernel `sim_argmax_kernel` in `csrc/sim_argmax.hip`,
 reached through the `gpa::sim_argmax` custom op.
 
+Any feature dim up to 4096 (the projected 128-d metric, and the unprojected
+1024-d metric of `metric_dim=0`, eval/eval_co3d.py:121-122).
 Numerics: fp32 accumulation of bf16 (or fp16) products; the max is taken over the fp32
 scores (not bf16-rounded scores as in the chunked torch path), and ties
 resolve to the lowest destination index, as the reference kernel's strict
@@ -20,8 +22,6 @@ import torch.nn.functional as F
 from . import _native
 
 __all__ = ["fused_similarity_argmax"]
-
-_MAX_D = 256
 
 
 def fused_similarity_argmax(a: torch.Tensor, b: torch.Tensor):
@@ -47,10 +47,6 @@ def fused_similarity_argmax(a: torch.Tensor, b: torch.Tensor):
     D = a.shape[-1]
     if b.shape[-1] != D:
         raise ValueError(f"feature dims differ: {D} vs {b.shape[-1]}")
-    if D > _MAX_D:
-        raise NotImplementedError(
-            f"fused_similarity_argmax: feature dim {D} > {_MAX_D} is not implemented on gfx950 "
-            "(use a metric projection, metric_dim <= 256)")
     if D % 32:
         # Zero features add nothing to any dot product, so padding is exact.
         pad = 32 - D % 32

@@ -60,7 +60,7 @@ def _sim(**kw):
     (dict(N=0), _native.GPA_E_INVALID),
     (dict(a=None), _native.GPA_E_INVALID),
     (dict(D=48), _native.GPA_E_UNSUPPORTED),
-    (dict(D=512, a_sm=512, b_sn=512), _native.GPA_E_UNSUPPORTED),
+    (dict(D=4128, a_sm=4128, b_sn=4128), _native.GPA_E_UNSUPPORTED),
     (dict(a_sm=100), _native.GPA_E_INVALID),
     (dict(a=FAKE + 2), _native.GPA_E_INVALID),
     (dict(M=100_000, N=100_000), _native.GPA_E_WORKSPACE),
