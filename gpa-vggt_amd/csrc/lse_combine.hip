@@ -11,7 +11,9 @@
 // reference permutes `oa` back to [B, H, N, D], rounds the two weights to the
 // activation dtype and combines in that dtype before transposing to
 // [B, N, C]; here the weights and the sum stay in fp32, one rounding to
-// bf16, and the output is written once in its final layout.
+// the output format, and the output is written once in its final layout.
+// Instantiated for bf16 and for fp16 operands (the fp16-autocast evaluation
+// stack); y has the operands' format.
 //
 // Operands are addressed per (b, h, s, p) with token n = s*P + p, so both the
 // frame-major and the token-major layouts (and views of them) are plain
@@ -38,6 +40,7 @@ struct CombineArgs {
   int64_t total;  // B * N * H * D / 8
 };
 
+template <bool F16>
 __global__ __launch_bounds__(kThreads) void lse_combine_kernel(CombineArgs a) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= a.total) return;
@@ -63,7 +66,8 @@ __global__ __launch_bounds__(kThreads) void lse_combine_kernel(CombineArgs a) {
   bf16x8 yv;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    yv[j] = (__bf16)__builtin_fmaf((float)xa[j], ca, (float)xb[j] * cb);
+    yv[j] = f32_to_half<F16>(
+        __builtin_fmaf(half_to_f32<F16>(xa[j]), ca, half_to_f32<F16>(xb[j]) * cb));
   *reinterpret_cast<bf16x8*>(a.y + b * a.y_b + n * a.y_n + h * a.y_h + dc * 8) = yv;
 }
 
@@ -72,27 +76,28 @@ __global__ __launch_bounds__(kThreads) void lse_combine_kernel(CombineArgs a) {
 
 using namespace gpa;
 
-extern "C" int gpa_lse_combine_bf16(const void* oa, const float* la, const void* ob,
-                                    const float* lb, void* y, int64_t B, int64_t H, int64_t N,
-                                    int64_t P, int64_t D, int64_t oa_b, int64_t oa_h,
-                                    int64_t oa_s, int64_t oa_p, int64_t la_b, int64_t la_h,
-                                    int64_t la_s, int64_t la_p, int64_t ob_b, int64_t ob_h,
-                                    int64_t ob_s, int64_t ob_p, int64_t lb_b, int64_t lb_h,
-                                    int64_t lb_s, int64_t lb_p, int64_t y_b, int64_t y_n,
-                                    int64_t y_h, void* stream) {
+namespace {
+
+template <bool F16>
+int lse_combine_run(const char* fn, const void* oa, const float* la, const void* ob,
+                    const float* lb, void* y, int64_t B, int64_t H, int64_t N, int64_t P,
+                    int64_t D, int64_t oa_b, int64_t oa_h, int64_t oa_s, int64_t oa_p,
+                    int64_t la_b, int64_t la_h, int64_t la_s, int64_t la_p, int64_t ob_b,
+                    int64_t ob_h, int64_t ob_s, int64_t ob_p, int64_t lb_b, int64_t lb_h,
+                    int64_t lb_s, int64_t lb_p, int64_t y_b, int64_t y_n, int64_t y_h,
+                    void* stream) {
   gpa_clear_error();
   if (B < 0 || H < 0 || N < 0 || P <= 0 || D < 0) {
-    gpa_set_error("gpa_lse_combine_bf16: negative size or P <= 0");
+    gpa_set_error("%s: negative size or P <= 0", fn);
     return GPA_E_INVALID;
   }
   if (B == 0 || H == 0 || N == 0 || D == 0) return GPA_OK;
   if (!oa || !la || !ob || !lb || !y) {
-    gpa_set_error("gpa_lse_combine_bf16: null pointer");
+    gpa_set_error("%s: null pointer", fn);
     return GPA_E_INVALID;
   }
   if (N % P != 0) {
-    gpa_set_error("gpa_lse_combine_bf16: N=%lld is not a multiple of P=%lld", (long long)N,
-                  (long long)P);
+    gpa_set_error("%s: N=%lld is not a multiple of P=%lld", fn, (long long)N, (long long)P);
     return GPA_E_INVALID;
   }
   const bool aligned = D % 8 == 0 && (uintptr_t)oa % 16 == 0 && (uintptr_t)ob % 16 == 0 &&
@@ -101,7 +106,7 @@ extern "C" int gpa_lse_combine_bf16(const void* oa, const float* la, const void*
                        ob_s % 8 == 0 && ob_p % 8 == 0 && y_b % 8 == 0 && y_n % 8 == 0 &&
                        y_h % 8 == 0;
   if (!aligned) {
-    gpa_set_error("gpa_lse_combine_bf16: D must be a multiple of 8 and rows 16-byte aligned");
+    gpa_set_error("%s: D must be a multiple of 8 and rows 16-byte aligned", fn);
     return GPA_E_INVALID;
   }
   CombineArgs a{};
@@ -119,15 +124,35 @@ extern "C" int gpa_lse_combine_bf16(const void* oa, const float* la, const void*
   a.total = B * N * H * (D / 8);
   const int64_t blocks = (a.total + kThreads - 1) / kThreads;
   if (blocks > 0x7fffffff) {
-    gpa_set_error("gpa_lse_combine_bf16: problem exceeds the grid limit");
+    gpa_set_error("%s: problem exceeds the grid limit", fn);
     return GPA_E_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(lse_combine_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+  hipLaunchKernelGGL(lse_combine_kernel<F16>, dim3((unsigned)blocks), dim3(kThreads), 0,
                      (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_lse_combine_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+#define GPA_COMBINE_ARGS                                                                   \
+  const void *oa, const float *la, const void *ob, const float *lb, void *y, int64_t B,    \
+      int64_t H, int64_t N, int64_t P, int64_t D, int64_t oa_b, int64_t oa_h, int64_t oa_s, \
+      int64_t oa_p, int64_t la_b, int64_t la_h, int64_t la_s, int64_t la_p, int64_t ob_b,  \
+      int64_t ob_h, int64_t ob_s, int64_t ob_p, int64_t lb_b, int64_t lb_h, int64_t lb_s,  \
+      int64_t lb_p, int64_t y_b, int64_t y_n, int64_t y_h, void *stream
+#define GPA_COMBINE_PASS                                                                   \
+  oa, la, ob, lb, y, B, H, N, P, D, oa_b, oa_h, oa_s, oa_p, la_b, la_h, la_s, la_p, ob_b,  \
+      ob_h, ob_s, ob_p, lb_b, lb_h, lb_s, lb_p, y_b, y_n, y_h, stream
+
+extern "C" int gpa_lse_combine_bf16(GPA_COMBINE_ARGS) {
+  return lse_combine_run<false>("gpa_lse_combine_bf16", GPA_COMBINE_PASS);
+}
+
+extern "C" int gpa_lse_combine_f16(GPA_COMBINE_ARGS) {
+  return lse_combine_run<true>("gpa_lse_combine_f16", GPA_COMBINE_PASS);
 }

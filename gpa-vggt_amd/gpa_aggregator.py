@@ -288,14 +288,20 @@ class GpaAttention(nn.Module):
             raise ValueError(f"frame_special: {N} tokens is not a multiple of {P}")
         q_f = q.view(B, H, S, P, D).permute(0, 2, 1, 3, 4).reshape(B * S, H, P, D)
         k5, v5 = k.view(B, H, S, P, D), v.view(B, H, S, P, D)
+        kp = self.cfg.broadcast_pool
+        if kp < 0:
+            # No shared set: plain attention over each frame's own tokens
+            # (attention.py:178-182).
+            k_f = k5.permute(0, 2, 1, 3, 4).reshape(B * S, H, P, D)
+            v_f = v5.permute(0, 2, 1, 3, 4).reshape(B * S, H, P, D)
+            out = attention_keybias(q_f, k_f, v_f, None, self.scale)
+            return out.reshape(B, S, H, P, D).permute(0, 1, 3, 2, 4).reshape(B, N, C)
         own_k = k5[:, :, :, pts:].permute(0, 2, 1, 3, 4).reshape(B * S, H, P - pts, D)
         own_v = v5[:, :, :, pts:].permute(0, 2, 1, 3, 4).reshape(B * S, H, P - pts, D)
         out_a, lse_a = attention_keybias(q_f, own_k, own_v, None, self.scale, return_lse=True)
         del own_k, own_v
-        kp = self.cfg.broadcast_pool
         if kp > 0:
-            pooled_k, pooled_v, pool_size, _ = torch.ops.gpa.pool_shared(
-                k, v, S, pts, g, kp, False)
+            pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, g, kp)
             if self.merge_log is not None:
                 self.merge_log.append({"kind": "pool", "frames": S, "pool_size": pool_size})
             sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
@@ -312,10 +318,32 @@ class GpaAttention(nn.Module):
         return combine_by_lse(out_a, lse_a, out_b, lse_b, S)
 
 
+POOL_KERNEL_MAX_SEEDS = 64      # seeds per frame the gpa::pool_shared kernel holds
+
+
+def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: int, kp: int,
+                    want_assign: bool = False):
+    """The pooled summaries of the shared set (attention.py:113-140) from
+    k, v [B, H, S*P, D]: the `gpa::pool_shared` kernel for up to 64 seeds per
+    frame (pool stride >= 5 at grid 37, the reference default 8 included);
+    above that (stride <= 4) the reference's own torch ops on the device
+    (`pool_shared_torch`).  Returns (pooled_k, pooled_v [B, H, S*npool, D],
+    size [B, H, S, npool] fp32, assign [B, H, S, grid*grid] or an empty tensor)."""
+    nh = -(-grid // kp)
+    if nh * nh <= POOL_KERNEL_MAX_SEEDS and k.dtype == torch.bfloat16:
+        return torch.ops.gpa.pool_shared(k, v, frames, pts, grid, kp, want_assign)
+    B, H, N, D = k.shape
+    P = N // frames
+    pk, pv, size, assign = pool_shared_torch(k.view(B, H, frames, P, D),
+                                             v.view(B, H, frames, P, D), pts, grid, kp)
+    return pk, pv, size, assign if want_assign else assign.new_empty(0)
+
+
 def pool_shared_torch(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid: int, kp: int):
     """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140),
-    restated with torch ops; the harness runs the `gpa::pool_shared` kernel,
-    and this restatement pins it in the tests.
+    restated with torch ops.  The harness runs the `gpa::pool_shared` kernel
+    up to 64 seeds per frame and this restatement above that (pool stride
+    <= 4 at grid 37); the tests pin the kernel against it.
 
     k5/v5 [B, H, S, P, D].  Seeds are the stride-kp lattice patches; every
     patch joins the seed whose key it matches best by cosine (per head), and

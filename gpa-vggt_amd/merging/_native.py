@@ -12,7 +12,7 @@ two custom ops:
     gpa::merge_heads(Tensor t, Tensor offsets, Tensor tokens, int slots,
                      bool mean) -> (Tensor out, Tensor size, Tensor log_size)
     gpa::lse_combine(Tensor out_a, Tensor lse_a, Tensor out_b, Tensor lse_b,
-                     int frames) -> Tensor y
+                     int frames) -> Tensor y              (bf16 or fp16)
     gpa::qk_norm_rope(Tensor qkv, Tensor ln_w, Tensor ln_b, float eps,
                       Tensor? pos, Tensor? rope_cs, int heads, bool q_f32,
                       bool k_f32) -> (Tensor q, Tensor k)
@@ -108,6 +108,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         lib.gpa_attn_keybias_bf16.argtypes[:-4] + [ctypes.c_float, _vp])   # no workspace
     lib.gpa_lse_combine_bf16.restype = ctypes.c_int
     lib.gpa_lse_combine_bf16.argtypes = [_vp] * 5 + [_i64] * 5 + [_i64] * 16 + [_i64] * 3 + [_vp]
+    lib.gpa_lse_combine_f16.restype = ctypes.c_int
+    lib.gpa_lse_combine_f16.argtypes = lib.gpa_lse_combine_bf16.argtypes
     lib.gpa_qk_norm_rope_bf16.restype = ctypes.c_int
     lib.gpa_qk_norm_rope_bf16.argtypes = [
         _vp, _i64, _i64, _i64, _i64,   # qkv, B, N, H, D
@@ -176,7 +178,7 @@ def exported_symbols() -> Tuple[str, ...]:
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
             "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
             "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16",
-            "gpa_attn_keybias_bf16_noalloc")
+            "gpa_attn_keybias_bf16_noalloc", "gpa_lse_combine_f16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -403,12 +405,14 @@ def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
                 lse_b: torch.Tensor, frames: int) -> torch.Tensor:
     """Merge the own-frame attention (out_a [B*S, H, P, D], lse_a [B*S, H, P])
     and the shared-set attention (out_b [B, H, S*P, D], lse_b [B, H, S*P]) by
-    their log2 LSE; returns y [B, S*P, H*D] bf16."""
+    their log2 LSE; returns y [B, S*P, H*D] in the outputs' dtype (bf16 or
+    fp16, the same for both)."""
     dev = _require_gpu(out_a, lse_a, out_b, lse_b)
     for name, t in (("out_a", out_a), ("out_b", out_b)):
-        if t.dtype != torch.bfloat16 or t.dim() != 4:
-            raise ValueError(f"gpa::lse_combine: {name} must be bf16 [.,H,.,D], got "
-                             f"{t.dtype} {tuple(t.shape)}")
+        if t.dtype not in (torch.bfloat16, torch.float16) or t.dtype != out_a.dtype \
+                or t.dim() != 4:
+            raise ValueError(f"gpa::lse_combine: {name} must be bf16 or fp16 (both alike) "
+                             f"[.,H,.,D], got {t.dtype} {tuple(t.shape)}")
     for name, t in (("lse_a", lse_a), ("lse_b", lse_b)):
         if t.dtype != torch.float32 or t.dim() != 3:
             raise ValueError(f"gpa::lse_combine: {name} must be fp32 [.,H,.], got "
@@ -425,7 +429,7 @@ def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
         out_a = out_a.contiguous()
     if not _rows_ok(out_b, 8):
         out_b = out_b.contiguous()
-    y = torch.empty(B, N, H * D, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(B, N, H * D, device=dev, dtype=out_a.dtype)
     if y.numel() == 0:
         return y
     sa0, sa1, sa2 = out_a.stride()[:3]
@@ -433,7 +437,9 @@ def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
     sb0, sb1, sb2 = out_b.stride()[:3]
     lb0, lb1, lb2 = lse_b.stride()
     with torch.cuda.device(dev):
-        rc = lib().gpa_lse_combine_bf16(
+        fn = lib().gpa_lse_combine_f16 if out_a.dtype == torch.float16 \
+            else lib().gpa_lse_combine_bf16
+        rc = fn(
             out_a.data_ptr(), lse_a.data_ptr(), out_b.data_ptr(), lse_b.data_ptr(), y.data_ptr(),
             B, H, N, P, D,
             S * sa0, sa1, sa0, sa2,            # out_a (b, h, s, p)
@@ -449,7 +455,7 @@ def lse_combine(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor,
 @lse_combine.register_fake
 def _lse_combine_fake(out_a, lse_a, out_b, lse_b, frames):
     B, H, N, D = out_b.shape
-    return out_b.new_empty(B, N, H * D, dtype=torch.bfloat16)
+    return out_b.new_empty(B, N, H * D, dtype=out_a.dtype)
 
 
 @torch.library.custom_op("gpa::qk_norm_rope", mutates_args=())

@@ -63,8 +63,9 @@ def combine_by_lse(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor
     queries over the frame's own keys (frame-major, as the own-frame call of
     vggt/layers/attention.py:157 returns it); out_b [B, H, S*P, D], lse_b
     [B, H, S*P]: attention of all queries over the shared keys (:162).  The
-    log2 LSEs weight the two (:166-176); returns [B, S*P, H*D] in bf16, the
-    layout the output projection takes.  The weights and the sum are fp32
-    (the reference rounds the weights to the activation dtype first).
+    log2 LSEs weight the two (:166-176); returns [B, S*P, H*D] in the
+    outputs' dtype (bf16 or fp16), the layout the output projection takes.
+    The weights and the sum are fp32 (the reference rounds the weights to the
+    activation dtype first).
     """
     return torch.ops.gpa.lse_combine(out_a, lse_a, out_b, lse_b, int(frames))

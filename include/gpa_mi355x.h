@@ -239,6 +239,17 @@ int gpa_lse_combine_bf16(const void* oa, const float* la, const void* ob, const 
                          int64_t lb_b, int64_t lb_h, int64_t lb_s, int64_t lb_p,
                          int64_t y_b, int64_t y_n, int64_t y_h, void* stream);
 
+/* The same on fp16 oa, ob and y (the combine under fp16 autocast, where the
+ * reference combines in the fp16 activation dtype, attention.py:166-176);
+ * weights and sums in fp32, one rounding to fp16. */
+int gpa_lse_combine_f16(const void* oa, const float* la, const void* ob, const float* lb,
+                        void* y, int64_t B, int64_t H, int64_t N, int64_t P, int64_t D,
+                        int64_t oa_b, int64_t oa_h, int64_t oa_s, int64_t oa_p,
+                        int64_t la_b, int64_t la_h, int64_t la_s, int64_t la_p,
+                        int64_t ob_b, int64_t ob_h, int64_t ob_s, int64_t ob_p,
+                        int64_t lb_b, int64_t lb_h, int64_t lb_s, int64_t lb_p,
+                        int64_t y_b, int64_t y_n, int64_t y_h, void* stream);
+
 /*
  * qk LayerNorm + 2D rotary embedding + cast, from the QKV projection rows.
  * For each token n < N of batch b and head h < H (D must be 64):

@@ -136,8 +136,14 @@ def test_merged_block_attention_matches_reference(dev):
     _compare(got, _proj_ref(blk, o), "merged block")
 
 
-def test_frame_special_block_attention_matches_reference(dev):
+@pytest.mark.parametrize("kp", [8, 5, 4, 0, -1])
+def test_frame_special_block_attention_matches_reference(dev, kp):
+    """The frame-special block for the pool strides the reference accepts
+    (attention.py:106-108, 178-190): kp > 0 pooled summaries (the kernel up
+    to 64 seeds, kp 8 and 5; the torch restatement above, kp 4), kp = 0 the
+    special tokens only, kp < 0 plain frame attention."""
     cfg, blk = _block(dev, seed=1)
+    cfg.broadcast_pool = kp
     blk.attn.frame_special = True
     x, pos, rope = _inputs(dev)
     N = x.shape[1]
@@ -146,29 +152,41 @@ def test_frame_special_block_attention_matches_reference(dev):
         got = blk.attn(xn, rope, None)
         # the device's pool assignment, from the module's own K/V
         _, kd, vd = blk.attn.qk(xn, rope)
-        _, _, size_d, assign_d = torch.ops.gpa.pool_shared(kd, vd, FRAMES, PTS, GRID, 8, True)
+        if kp > 0:
+            _, _, size_d, assign_d = A.pool_shared_set(kd, vd, FRAMES, PTS, GRID, kp, True)
     q, k, v = _qkv_ref(blk, xn, pos)
     q16, k16, v16 = q.bfloat16().float(), k.bfloat16().float(), v
     k5, v5 = k16.view(1, 16, FRAMES, P, 64), v16.view(1, 16, FRAMES, P, 64)
-    assign = assign_d.cpu().long()
-    npool = 25
-    onehot = F.one_hot(assign, npool).double()                     # [1,16,S,1369,25]
-    cnt = onehot.sum(3)                                            # [1,16,S,25]
-    assert torch.equal(cnt.float(), size_d.cpu())
-    pk = torch.einsum("bhspg,bhspd->bhsgd", onehot, k5[:, :, :, PTS:].double()) / cnt[..., None]
-    pv = torch.einsum("bhspg,bhspd->bhsgd", onehot, v5[:, :, :, PTS:].double()) / cnt[..., None]
+    out = torch.empty(1, 16, N, 64)
+    if kp < 0:
+        for s in range(FRAMES):
+            o, _ = attention_reference(*kernel_inputs(q16[:, :, s * P:(s + 1) * P], k5[:, :, s],
+                                                      v5[:, :, s], None), blk.attn.scale)
+            out[:, :, s * P:(s + 1) * P] = o
+        _compare(got, _proj_ref(blk, out), f"frame attention (kp {kp})")
+        return
     sp_k = k5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
     sp_v = v5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
-    out = torch.empty(1, 16, N, 64)
+    extra_k, extra_v, extra_b = [sp_k], [sp_v], [torch.zeros(1, 16, 1, FRAMES * PTS)]
+    if kp > 0:
+        assign = assign_d.cpu().long()
+        npool = (-(-GRID // kp)) ** 2
+        onehot = F.one_hot(assign, npool).double()                     # [1,16,S,1369,np]
+        cnt = onehot.sum(3)                                            # [1,16,S,np]
+        assert torch.equal(cnt.float(), size_d.cpu())
+        pk = torch.einsum("bhspg,bhspd->bhsgd", onehot, k5[:, :, :, PTS:].double()) / cnt[..., None]
+        pv = torch.einsum("bhspg,bhspd->bhsgd", onehot, v5[:, :, :, PTS:].double()) / cnt[..., None]
+        extra_k.append(pk.reshape(1, 16, -1, 64).float())
+        extra_v.append(pv.reshape(1, 16, -1, 64).float())
+        extra_b.append(cnt.reshape(1, 16, 1, -1).log().float())
     for s in range(FRAMES):
-        kk = torch.cat([k5[:, :, s, PTS:], sp_k, pk.reshape(1, 16, -1, 64).float()], dim=2)
-        vv = torch.cat([v5[:, :, s, PTS:], sp_v, pv.reshape(1, 16, -1, 64).float()], dim=2)
-        bias = torch.zeros(1, 16, 1, kk.shape[2])
-        bias[..., GRID * GRID + FRAMES * PTS:] = cnt.reshape(1, 16, -1).log().float()[:, :, None]
+        kk = torch.cat([k5[:, :, s, PTS:]] + extra_k, dim=2)
+        vv = torch.cat([v5[:, :, s, PTS:]] + extra_v, dim=2)
+        bias = torch.cat([torch.zeros(1, 16, 1, GRID * GRID)] + extra_b, dim=3)
         o, _ = attention_reference(*kernel_inputs(q16[:, :, s * P:(s + 1) * P], kk, vv, bias),
                                    blk.attn.scale)
         out[:, :, s * P:(s + 1) * P] = o
-    _compare(got, _proj_ref(blk, out), "frame-special block")
+    _compare(got, _proj_ref(blk, out), f"frame-special block (kp {kp})")
 
 
 def test_small_aggregator_runs_every_global_path(dev):

@@ -28,14 +28,14 @@ pytestmark = pytest.mark.gpu
 SCALE = 0.125
 
 
-def _split_inputs(B, S, H, P, pts, npool, seed, scale=0.5):
+def _split_inputs(B, S, H, P, pts, npool, seed, scale=0.5, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     N = S * P
-    q = (torch.randn(B, H, N, 64, generator=g) * scale).bfloat16()
-    k = (torch.randn(B, H, N, 64, generator=g) * scale).bfloat16()
-    v = torch.randn(B, H, N, 64, generator=g).bfloat16()
-    pk = (torch.randn(B, H, S * npool, 64, generator=g) * scale).bfloat16()
-    pv = torch.randn(B, H, S * npool, 64, generator=g).bfloat16()
+    q = (torch.randn(B, H, N, 64, generator=g) * scale).to(dtype)
+    k = (torch.randn(B, H, N, 64, generator=g) * scale).to(dtype)
+    v = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    pk = (torch.randn(B, H, S * npool, 64, generator=g) * scale).to(dtype)
+    pv = torch.randn(B, H, S * npool, 64, generator=g).to(dtype)
     psize = torch.randint(1, 9, (B, H, S * npool), generator=g).float()
     return q, k, v, pk, pv, psize
 
@@ -52,7 +52,7 @@ def _split_path(q, k, v, pk, pv, psize, S, P, pts):
     sh_v = torch.cat([v5[:, :, :, :pts].reshape(B, H, S * pts, D), pv], dim=2)
     sh_bias = torch.zeros(B, H, 1, sh_k.shape[2], device=q.device)
     sh_bias[:, :, 0, S * pts:] = psize.log()
-    out_b, lse_b = attention_keybias(q, sh_k, sh_v, sh_bias.bfloat16(), SCALE, return_lse=True)
+    out_b, lse_b = attention_keybias(q, sh_k, sh_v, sh_bias.to(q.dtype), SCALE, return_lse=True)
     return combine_by_lse(out_a, lse_a, out_b, lse_b, S), (out_a, lse_a, out_b, lse_b)
 
 
@@ -71,18 +71,21 @@ def _full_reference(q, k, v, pk, pv, psize, S, P, pts, frames=None, rows=None):
         vf = torch.cat([v5[:, :, f, pts:], sp_v, pv], dim=2)
         bias = torch.zeros(B, H, 1, kf.shape[2])
         bias[:, :, 0, kf.shape[2] - pk.shape[2]:] = psize.log()
-        o, _ = attention_reference(qf, kf, vf, bias.bfloat16(), SCALE)
+        o, _ = attention_reference(qf, kf, vf, bias.to(q.dtype), SCALE)
         outs[f] = o                                  # [B, H, rows, D]
     return outs
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,S,H,P,pts,npool", [(1, 4, 2, 41, 5, 9), (2, 3, 3, 70, 5, 16),
                                                 (1, 6, 4, 1374, 5, 25)])
-def test_split_path_matches_full_attention(dev, B, S, H, P, pts, npool):
-    q, k, v, pk, pv, psize = _split_inputs(B, S, H, P, pts, npool, seed=S * P + H)
+def test_split_path_matches_full_attention(dev, B, S, H, P, pts, npool, dtype):
+    """bf16, and fp16 as under the fp16-autocast evaluation stack (the
+    attention kernels and the combine all in fp16)."""
+    q, k, v, pk, pv, psize = _split_inputs(B, S, H, P, pts, npool, seed=S * P + H, dtype=dtype)
     y, _ = _split_path(q.to(dev), k.to(dev), v.to(dev), pk.to(dev), pv.to(dev), psize.to(dev),
                        S, P, pts)
-    assert y.shape == (B, S * P, H * 64) and y.dtype == torch.bfloat16
+    assert y.shape == (B, S * P, H * 64) and y.dtype == dtype
     ref = _full_reference(q, k, v, pk, pv, psize, S, P, pts)
     yc = y.float().cpu().view(B, S, P, H, 64)
     errs = [(yc[:, f].permute(0, 2, 1, 3) - ref[f]).abs() for f in range(S)]
@@ -90,21 +93,24 @@ def test_split_path_matches_full_attention(dev, B, S, H, P, pts, npool):
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3, (err.max(), err.mean())
 
 
-def test_combine_matches_oracle(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_combine_matches_oracle(dev, dtype):
     g = torch.Generator().manual_seed(9)
     B, S, H, P, D = 2, 3, 4, 50, 64
     N = S * P
-    out_a = torch.randn(B * S, H, P, D, generator=g).bfloat16()
-    out_b = torch.randn(B, H, N, D, generator=g).bfloat16()
+    out_a = torch.randn(B * S, H, P, D, generator=g).to(dtype)
+    out_b = torch.randn(B, H, N, D, generator=g).to(dtype)
     lse_a = torch.randn(B * S, H, P, generator=g) * 20
     lse_b = torch.randn(B, H, N, generator=g) * 20
     y = combine_by_lse(out_a.to(dev), lse_a.to(dev), out_b.to(dev), lse_b.to(dev), S).cpu()
     oa = out_a.float().view(B, S, H, P, D).permute(0, 2, 1, 3, 4).reshape(B, H, N, D)
     la = lse_a.view(B, S, H, P).permute(0, 2, 1, 3).reshape(B, H, N)
     ref = lse_combine(oa, la, out_b.float(), lse_b).transpose(1, 2).reshape(B, N, H * D)
+    assert y.dtype == dtype
     err = (y.float() - ref).abs()
-    # one bf16 rounding of values of magnitude <~ 4
-    assert err.max().item() <= 2.0 ** -8 * ref.abs().max().item() + 1e-6
+    # one rounding to the output format of values of magnitude <~ 4
+    ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    assert err.max().item() <= ulp * ref.abs().max().item() + 1e-6
 
 
 def test_combine_accepts_strided_views(dev):
@@ -131,6 +137,8 @@ def test_combine_argument_checks(dev):
         combine_by_lse(oa, la, ob, lb, 3)                  # frames do not divide
     with pytest.raises(ValueError):
         combine_by_lse(oa.float(), la, ob, lb, 2)          # dtype
+    with pytest.raises(ValueError):
+        combine_by_lse(oa.half(), la, ob, lb, 2)           # mixed bf16 / fp16
 
 
 def test_200_frame_shapes_on_a_sample(dev):
