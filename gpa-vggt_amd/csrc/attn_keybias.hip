@@ -17,10 +17,10 @@
 //     32-query blocks, <= 256 VGPRs each, so two workgroups share a CU (two
 //     waves per SIMD).  Each K or V fragment read from LDS serves both of a
 //     wave's blocks.
-//   * Two passes.  The main pass (attn_main_kernel) runs every wave with a
-//     fixed softmax offset certified on tile 0 and software-pipelines its
-//     tiles (see there); the rare waves it cannot certify are recomputed by
-//     the repair pass (attn_repair_kernel) with a lazily moved offset.
+//   * One pass (attn_main_kernel), software-pipelined by one tile.  Every
+//     wave runs with a fixed softmax offset certified on tile 0; a wave that
+//     cannot certify it continues in place with a lazily moved offset (see
+//     there), so no work is discarded or recomputed.
 //   * K, V and the tile records stream through an LDS ring of 32-key tiles
 //     filled by buffer_load ... lds (DMA into LDS, no staging registers)
 //     several tiles ahead of the one being computed; keeping three tiles in
@@ -43,14 +43,12 @@
 //     rescale is a per-lane multiply.
 //   * The softmax offset m only has to keep 2^(x-m) in range, since P is
 //     stored in bf16, which has fp32's exponent range (fp16 P stops at 65504,
-//     hence kTau = 15 there): m moves lazily, only when a tile could produce
-//     x > m + kTau.  Whether it could is decided
-//     from a Cauchy-Schwarz bound, x <= c*(|q| max|k| + max bias/sm_scale)
-//     over the tile's keys (the record carries both maxima), one FMA per
-//     lane; only when the bound exceeds m + kTau does the wave take the exact
-//     row max and, where it is above m + kTau, rescale (a rare, wave-uniform
-//     branch).  The result is the same softmax; only the (arbitrary) offset
-//     differs from the reference's running max.
+//     hence P <= 2^15 there): either a fixed offset derived from a
+//     Cauchy-Schwarz bound on the scores, x <= c*(|q| max|k| + max
+//     bias/sm_scale) (the tile records carry both maxima), or, where that
+//     bound is too loose for the row, an offset that moves only when a tile's
+//     exact max rises above m + kUp.  The result is the same softmax; only the
+//     (arbitrary) offset differs from the reference's running max.
 //   * Row sums add up the bf16 P the P.V product uses, on the matrix pipe:
 //     v_mfma_f32_4x4x4_16b_bf16 with an all-ones A operand adds each lane's
 //     four B values into its fp32 accumulator (four per block and tile).
@@ -85,18 +83,16 @@ constexpr int kQPerWave = 32 * kBlk;
 constexpr int kQPerWG = kWaves * kQPerWave;   // 256 queries per workgroup
 constexpr int kKT = 32;                       // keys per tile
 constexpr int kHD = 64;                       // head dim
-constexpr int kRing = 4;                      // LDS tile slots
-constexpr int kAhead = kRing - 1;             // tiles in flight beyond the current one
-// Lazy rescale threshold (log2), P <= 2^kTau: bf16 has fp32's exponent
-// range; fp16's largest value is 65504 < 2^16.
-template <bool F16> constexpr float kTau = F16 ? 15.0f : 16.0f;
 constexpr float kMInit = -1.0e30f;            // finite initial offset (all -inf rows give 0)
-// Fixed offset of the main pass: m = bound - kShift, certified when the row
-// max is within kGap of the bound.  bf16 P keeps fp32's exponent range, so
-// the gap may be wide; fp16 P sits in [2^(kShift-kGap), 2^kShift] =
-// [2^-1, 2^15], far from fp16's subnormals and below its 65504.
-template <bool F16> constexpr float kGap = F16 ? 16.0f : 64.0f;
-template <bool F16> constexpr float kShift = F16 ? 15.0f : 0.0f;
+// Offset window (log2 units).  Every P stays <= 2^kUp: for bf16 P (fp32's
+// exponent range) 2^64 leaves row sums and O far below fp32's 2^128 for any
+// key count and value size; fp16 P must stay below 65504.  A fixed offset is
+// certified when each row's largest P is >= 2^-kDown: for bf16 2^-96 keeps
+// every term that matters to 24 bits above fp32's normal range; for fp16 the
+// largest P stays >= 2^-1, far from fp16's subnormals.  The lazily moved
+// offset keeps the largest P in [1, 2^kUp].
+template <bool F16> constexpr float kUp = F16 ? 15.0f : 64.0f;
+template <bool F16> constexpr float kDown = F16 ? 1.0f : 96.0f;
 constexpr int kRec = 36;                      // words per tile record
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -106,7 +102,7 @@ struct AttnArgs {
   const uint16_t* v;
   const float* recs;      // [B*H][ntiles][kRec] tile records
   const float* bounds;    // [B*H][2] maxima of the records' words 32 and 33
-  uint8_t* flags;         // [B*H][gx][kWaves] per wave: 1 = rows left to the repair pass
+  uint8_t* flags;         // [B*H][gx][kWaves] per wave: 1 = the lazily moved offset ran
   uint16_t* o;
   float* lse;
   int H;
@@ -128,15 +124,6 @@ struct RecArgs {
   int64_t total;  // B * H * ntiles
   float mul;  // 1 / sm_scale
   float c;    // sm_scale * log2(e)
-};
-
-// One slot of the tile ring.
-struct alignas(16) Tile {
-  uint16_t k[kKT * kHD];  // key rows, 16-byte chunks swizzled by k_chunk
-  uint16_t v[kKT * kHD];  // value rows, 16-byte chunks swizzled by v_chunk
-  // [0, 32): bias/sm_scale per key; [32]: c*max|k|; [33]: c*max bias/sm_scale;
-  // [34, 36): zero.
-  float rec[kRec];
 };
 
 // K chunk swizzle: 16 consecutive keys reading one logical chunk hit 16
@@ -304,279 +291,7 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// The repair pass, for the waves the main pass (attn_main_kernel below) could
-// not certify.  Workgroups without a flagged wave exit at once; the others
-// recompute their rows with a lazily moved offset, and the flagged waves
-// store theirs.
-template <bool F16>
-__global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
-  // Four separate LDS objects (not one array) so the compiler's LDS-DMA
-  // tracking can tell which slot a DMA writes and which a read reads.
-  __shared__ Tile ring0, ring1, ring2, ring3;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, hi = lane >> 5, l32 = lane & 31;
-  // Wave index in an SGPR: the DMA's LDS base (M0) must be wave-uniform.
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bh = blockIdx.y;
-  const int64_t b = bh / p.H, h = bh % p.H;
-  uint8_t* const flag_row = p.flags + ((int64_t)bh * gridDim.x + blockIdx.x) * kWaves;
-  const uint32_t flags4 = *reinterpret_cast<const uint32_t*>(flag_row);
-  if (flags4 == 0) return;  // workgroup-uniform: before any barrier or DMA
-  const bool store = ((flags4 >> (8 * wave)) & 0xff) != 0;
-  const int64_t q_base = (int64_t)blockIdx.x * kQPerWG + wave * kQPerWave + l32;
-  const float c = p.c;
-
-  const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
-  const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
-  const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
-
-  // Q^T as the B-operand of S^T = K . Q^T: in block j the lane supplies
-  // query q_base + 32 j, features 16*ks + 8*hi .. +8.  |q| feeds the bound.
-  bf16x8 qf[kBlk][4];
-  float q_norm[kBlk];
-#pragma unroll
-  for (int j = 0; j < kBlk; ++j) {
-    const int64_t row = q_base + 32 * j;
-    float ss = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
-                            : bf16x8{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = half_to_f32<F16>(qf[j][ks][e]);
-        ss = __builtin_fmaf(f, f, ss);
-      }
-    }
-    q_norm[j] = __builtin_sqrtf(sum_halves(ss));
-  }
-
-  // DMA roles: wave w copies the w-th kilobyte of the K tile and of the V
-  // tile (keys 8w..8w+7); lanes 0-8 of wave 0 also copy the 144-byte tile
-  // record.  Each lane fetches the global chunk that belongs in its LDS slot
-  // under the swizzle.
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
-  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(R, p.rec_bytes);
-  const uint32_t k_row = (uint32_t)p.k_sn * 2u, v_row = (uint32_t)p.v_sn * 2u;
-  const int slot = wave * 64 + lane;  // 16-byte slot within the K or V tile
-  const int s_key = slot >> 3, s_pc = slot & 7;
-  const uint32_t k_voff = s_key * k_row + k_chunk(s_key, s_pc) * 16;
-  const uint32_t v_voff = s_key * v_row + v_chunk(s_key, s_pc) * 16;
-  const int ntiles = (int)((p.N + kKT - 1) / kKT);
-  const __bf16 one = f32_to_half<F16>(1.0f);
-  const bf16x4 ones4 = {one, one, one, one};
-
-  auto issue = [&](int t, Tile& T) {
-    const uint32_t n0 = (uint32_t)t * kKT;
-    dma16(krs, &T.k[wave * 512], k_voff, n0 * k_row);
-    dma16(vrs, &T.v[wave * 512], v_voff, n0 * v_row);
-    if (wave == 0 && lane < kRec / 4) dma16(rrs, &T.rec[0], lane * 16, (uint32_t)t * (kRec * 4));
-  };
-  // Tile t+1 has landed once only tiles t+2 and t+3 are outstanding: three
-  // DMA instructions per tile on wave 0, two on the others.
-  auto wait_next = [&]() {
-    if (wave == 0)
-      wait_vm<3 * (kAhead - 1)>();
-    else
-      wait_vm<2 * (kAhead - 1)>();
-  };
-
-  // Per-lane LDS element offsets of the fragment reads (slot-independent).
-  int k_off[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) k_off[ks] = l32 * kHD + (k_chunk(l32, 2 * ks + hi) << 3);
-  // V^T transpose reads: block db (features 32db..), k-step s, part pp
-  // (keys 16s + 8pp + 4hi + 0..3).  Within its 16-lane group this lane is
-  // the source of key offset (lane&15)>>2 and feature quad lane&3.  The
-  // swizzle depends on key&3 only, which s and pp leave unchanged, so those
-  // two are constant offsets (1024 s + 512 pp elements) from one base per db.
-  int v_base[2];
-#pragma unroll
-  for (int db = 0; db < 2; ++db) {
-    const int key = 4 * hi + ((lane & 15) >> 2);
-    const int a = lane & 3;
-    const int ch = db * 4 + ((lane >> 4) & 1) * 2 + (a >> 1);
-    v_base[db] = key * kHD + (v_chunk(key, ch) << 3) + (a & 1) * 4;
-  }
-
-  float m_run[kBlk];
-  f32x4 l_acc[kBlk];
-  f32x16 o_acc[kBlk][2];
-#pragma unroll
-  for (int j = 0; j < kBlk; ++j) {
-    m_run[j] = kMInit;
-    l_acc[j] = f32x4{};
-    o_acc[j][0] = f32x16{};
-    o_acc[j][1] = f32x16{};
-  }
-
-  // One tile: fetch tile t+3 into the slot tile t-1 used, compute tile t for
-  // both query blocks, wait until tile t+1 has landed, synchronise.  The
-  // offset m starts at tile 0's row max (kFirst) and then moves lazily
-  // (kLazy): x <= c*(|q| max|k| + max bias/sm_scale) over the tile; only
-  // when that bound exceeds m + kTau can 2^(x-m) leave [0, 2^kTau]: then
-  // take the exact row max and move m where it is above m + kTau, rescaling
-  // what has been accumulated.
-  constexpr int kFirst = 0, kLazy = 2;
-  auto step = [&](auto mode, const int t, const Tile& T, Tile& Tfree) {
-    constexpr int MODE = decltype(mode)::value;
-    issue(t + kAhead, Tfree);
-
-    // Scores s = q.k + bias/sm_scale: both blocks' accumulators (rows
-    // 8g + 4hi + i of the 32x32 result) start from the keys' bias values,
-    // and each K fragment serves both blocks.
-    f32x16 bias16;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(&T.rec[8 * g + 4 * hi]);
-      bias16[4 * g + 0] = bv[0];
-      bias16[4 * g + 1] = bv[1];
-      bias16[4 * g + 2] = bv[2];
-      bias16[4 * g + 3] = bv[3];
-    }
-    f32x16 sv[kBlk];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&T.k[k_off[ks]]);
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j)
-        sv[j] = mfma32x32x16_t<F16>(kf, qf[j][ks], ks == 0 ? bias16 : sv[j]);
-    }
-
-    // V^T fragments of this tile, shared by both blocks.
-    bf16x8 vf[2][2];
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        typedef short i16x4 __attribute__((ext_vector_type(4)));
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s]);
-        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&T.v[v_base[db] + 1024 * s + 512]);
-        const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
-        vf[db][s] = bf16x8{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
-      }
-
-    auto tile_max = [&](const f32x16& x) {
-      float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
-#pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
-      mx = fmaxf(mx, x[15]);
-      return max_halves(mx) * c;
-    };
-    if constexpr (MODE == kFirst) {
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j) m_run[j] = fmaxf(tile_max(sv[j]), kMInit);
-    } else if constexpr (MODE == kLazy) {
-      // (One branch level per block: nested ones make the register
-      // allocator copy the O accumulators on every tile.)
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j) {
-        const float ub = __builtin_fmaf(q_norm[j], T.rec[kKT], T.rec[kKT + 1]);
-        if (__builtin_amdgcn_ballot_w64(ub > m_run[j] + kTau<F16>) != 0) {
-          const float ms = tile_max(sv[j]);
-          const float m_new = ms > m_run[j] + kTau<F16> ? ms : m_run[j];
-          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
-          m_run[j] = m_new;
-          l_acc[j] *= alpha;
-          o_acc[j][0] *= alpha;
-          o_acc[j][1] *= alpha;
-        }
-      }
-    }
-
-    // P = 2^(s*c - m) in bf16, row sums, then O^T += V^T . P^T; the V^T
-    // operand of k-step s covers the keys whose probabilities this lane
-    // holds in its score registers 8s..8s+7.  The row sums of the bf16 P
-    // run on the matrix pipe: a 4x4x4 MFMA with an all-ones A operand adds
-    // each lane's four B values into its accumulator.
-#pragma unroll
-    for (int j = 0; j < kBlk; ++j) {
-      const float neg_m = -m_run[j];
-      bf16x8 pb[2];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e], c, neg_m));
-          const float p1 =
-              __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j][8 * half + e + 1], c, neg_m));
-          const bf16x2 pv = pack2<F16>(p0, p1);
-          pb[half][e] = pv[0];
-          pb[half][e + 1] = pv[1];
-        }
-        const bf16x4 lo = {pb[half][0], pb[half][1], pb[half][2], pb[half][3]};
-        const bf16x4 up = {pb[half][4], pb[half][5], pb[half][6], pb[half][7]};
-        l_acc[j] = mfma4x4x4_t<F16>(ones4, lo, l_acc[j]);
-        l_acc[j] = mfma4x4x4_t<F16>(ones4, up, l_acc[j]);
-      }
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          o_acc[j][db] = mfma32x32x16_t<F16>(vf[db][s], pb[s], o_acc[j][db]);
-    }
-
-    wait_next();
-    tile_barrier();
-  };
-
-  // Prologue: tiles 0..2 in flight; wait for tile 0.
-  issue(0, ring0);
-  issue(1, ring1);
-  issue(2, ring2);
-  wait_next();
-  tile_barrier();
-
-  step(std::integral_constant<int, kFirst>{}, 0, ring0, ring3);
-  // Tiles 1.. four per trip, so every slot is a compile-time LDS object.
-  auto run = [&](auto mode) {
-    int t = 1;
-    for (; t + 4 <= ntiles; t += 4) {
-      step(mode, t, ring1, ring0);
-      step(mode, t + 1, ring2, ring1);
-      step(mode, t + 2, ring3, ring2);
-      step(mode, t + 3, ring0, ring3);
-    }
-    if (t < ntiles) step(mode, t++, ring1, ring0);
-    if (t < ntiles) step(mode, t++, ring2, ring1);
-    if (t < ntiles) step(mode, t++, ring3, ring2);
-  };
-  run(std::integral_constant<int, kLazy>{});
-  // Drain the DMAs still in flight before the workgroup can exit.
-  wait_vm<0>();
-
-  // Epilogue: combine the two key halves of the row sums, normalise, store.
-  if (!store) return;
-  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
-#pragma unroll
-  for (int j = 0; j < kBlk; ++j) {
-    const int64_t row = q_base + 32 * j;
-    const float l_tot = sum_halves(l_acc[j][0]);
-    const float inv = 1.0f / l_tot;
-    if (row < p.M) {
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          const bf16x4 ov = {f32_to_half<F16>(o_acc[j][db][4 * g + 0] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 1] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 2] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 3] * inv)};
-          *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
-        }
-      if (p.lse && hi == 0)
-        p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_run[j] + __log2f(l_tot);
-    }
-  }
-}
-
-// The main pass: the fixed softmax offset, software-pipelined by one tile.
+// The attention kernel: software-pipelined by one tile.
 //
 // On gfx950 a wave's MFMAs overlap its own VALU work well (measured: 16
 // MFMAs of 32x32x16 interleaved with a tile's softmax in one wave run at
@@ -591,11 +306,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 // instructions, after the iteration's LDS reads.  Only the last block's
 // P.V product has no VALU work beside it.
 //
-// The offset is the fixed one: m = c*(|q| max|k| + max bias/sm_scale) over
-// all keys (Cauchy-Schwarz), certified per wave on tile 0 (every row max is
-// within kGap of m, so the keys that matter keep probabilities far above
-// fp32's normal range).  A wave that cannot certify it stores nothing and
-// sets its flag for the repair pass.
+// The softmax offset.  B = c*(|q| max|k| + max bias/sm_scale) over all keys
+// bounds every score of a row (Cauchy-Schwarz).  From tile 0's exact row
+// max x0 the wave takes the fixed offset m = max(B - kUp, x0): no score can
+// then produce P above 2^kUp, and the wave is certified when every row has
+// x0 >= m - kDown, i.e. the row's largest P is at least 2^-kDown.  A
+// certified wave runs the loop with no max, rescale or branch at all.  A wave
+// that cannot certify (B far above the row's real scores: sharp logits, or
+// fp16's narrow window) runs a second loop with a lazily moved offset
+// instead: m starts at x0 and, per tile, S(t), its exact row max, a
+// wave-uniform branch that rescales O and the row sums only where that max
+// exceeds m + kUp, then P(t) and its P.V product.  That loop is not
+// pipelined (S(t) and P(t) in the same iteration), so it holds fewer live
+// registers than the certified loop and leaves its register allocation and
+// schedule as they are.  Both loops issue the same DMAs, waits and barriers.
+// The per-wave flag records which loop ran (1 = lazy offset).
 //
 // Five ring slots keep tile t (V), tile t+1 (K, bias) and the three tiles
 // in flight; the DMA of tile t+4 refills the slot of tile t-1.  Every wave
@@ -606,7 +331,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_repair_kernel(AttnArgs p) {
 // unrolled iterations then form one basic block, in which the pure
 // arithmetic of an iteration could float down to its consumers in the next
 // one; an empty asm that takes the iteration's results as operands keeps it
-// inside.  250 VGPRs, two waves per SIMD.
+// inside.  At most 256 VGPRs, two waves per SIMD.
 constexpr int kMainSlots = 5;
 constexpr int kMainAhead = kMainSlots - 1;  // tiles issued ahead of the one being softmaxed
 
@@ -646,7 +371,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
   const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
 
-  // Q^T as the B-operand of S^T = K . Q^T (as in the repair pass).
+  // Q^T as the B-operand of S^T = K . Q^T: in block j the lane supplies
+  // query q_base + 32 j, features 16*ks + 8*hi .. +8.  |q| feeds the bound.
   bf16x8 qf[kBlk][4];
   float q_norm[kBlk];
 #pragma unroll
@@ -714,7 +440,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     l_acc[j] = f32x4{};
     o_acc[j][0] = f32x16{};
     o_acc[j][1] = f32x16{};
-    m_off[j] = __builtin_fmaf(q_norm[j], row_k, row_b) - kShift<F16>;
   }
 
   // S(T) for both blocks; the accumulators start from the keys' bias values.
@@ -750,6 +475,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
         const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
         vf[db][s] = bf16x8{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
       }
+  };
+  // Exact row max of a block's scores, in log2 units: the row's 16 keys in
+  // this lane and 16 in lane^32.
+  auto row_max = [&](const f32x16& x) {
+    float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
+    mx = fmaxf(mx, x[15]);
+    return max_halves(mx) * c;
   };
   // P = 2^(S c - m) of one block in bf16, its row sums, then O += V^T . P.
   const __bf16 one = f32_to_half<F16>(1.0f);
@@ -847,13 +581,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
-    float mx = fmaxf(fmaxf(s_cur[j][0], s_cur[j][1]), s_cur[j][2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s_cur[j][r]), s_cur[j][r + 1]);
-    mx = fmaxf(mx, s_cur[j][15]);
-    bad = bad || !(m_off[j] - max_halves(mx) * c <= kGap<F16> - kShift<F16>);
+    const float x0 = row_max(s_cur[j]);
+    m_off[j] = fmaxf(__builtin_fmaf(q_norm[j], row_k, row_b) - kUp<F16>, x0);
+    bad = bad || !(x0 >= m_off[j] - kDown<F16>);     // NaN scores fail too
   }
   const bool fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+  if (!fixed) {
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) m_off[j] = kMInit;   // the first tile moves it
+  }
   wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
   tile_barrier();
 
@@ -882,24 +618,62 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) s_cur[j] = s_nxt[j];
   };
+  // The lazily moved offset: tile t whole (its K and V are both resident in
+  // iteration t), with the same DMA, wait and barrier as `iter`.
+  auto lazy_iter = [&](const int t, const MainTile& Tcur, MainTile& Tissue) {
+    issue(t + kMainAhead, Tissue);
+    f32x16 sv[kBlk];
+    scores(Tcur, sv);
+    bf16x8 vf[2][2];
+    read_v(Tcur, vf);
+    // (One branch level per block: nested ones make the register allocator
+    // copy the O accumulators on every tile.)
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const float mx = row_max(sv[j]);
+      if (__builtin_amdgcn_ballot_w64(mx > m_off[j] + kUp<F16>) != 0) {
+        const float m_new = mx > m_off[j] + kUp<F16> ? mx : m_off[j];
+        const float alpha = __builtin_amdgcn_exp2f(m_off[j] - m_new);
+        m_off[j] = m_new;
+        l_acc[j] *= alpha;
+        o_acc[j][0] *= alpha;
+        o_acc[j][1] *= alpha;
+      }
+    }
+    softmax_pv(sv[0], 0, vf);
+    softmax_pv(sv[1], 1, vf);
+    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    tile_barrier();
+  };
   // Unrolled by the ring size, so every slot is a compile-time LDS object
   // (the waitcnt pass can then tell a slot being read from one being filled).
-  int t = 0;
-  for (; t + kMainSlots <= ntiles; t += kMainSlots) {
+  auto run = [&](auto lazy) {
+    constexpr bool LAZY = decltype(lazy)::value;
+    auto step = [&](const int t, const int u) {
+      if constexpr (LAZY)
+        lazy_iter(t, *ring[u], *ring[(u + kMainAhead) % kMainSlots]);
+      else
+        iter(t, *ring[u], *ring[(u + 1) % kMainSlots], *ring[(u + kMainAhead) % kMainSlots]);
+    };
+    int t = 0;
+    for (; t + kMainSlots <= ntiles; t += kMainSlots) {
 #pragma unroll
-    for (int u = 0; u < kMainSlots; ++u)
-      iter(t + u, *ring[u], *ring[(u + 1) % kMainSlots], *ring[(u + kMainAhead) % kMainSlots]);
-  }
-#pragma unroll
-  for (int u = 0; u < kMainSlots - 1; ++u)
-    if (t < ntiles) {
-      iter(t, *ring[u], *ring[(u + 1) % kMainSlots], *ring[(u + kMainAhead) % kMainSlots]);
-      ++t;
+      for (int u = 0; u < kMainSlots; ++u) step(t + u, u);
     }
+#pragma unroll
+    for (int u = 0; u < kMainSlots - 1; ++u)
+      if (t < ntiles) {
+        step(t, u);
+        ++t;
+      }
+  };
+  if (fixed)
+    run(std::false_type{});
+  else
+    run(std::true_type{});
   if (lane == 0) flag_row[wave] = fixed ? 0 : 1;
   // Drain the DMAs still in flight before the workgroup can exit.
   wait_vm<0>();
-  if (!fixed) return;
 
   uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
 #pragma unroll
@@ -1101,7 +875,6 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
   hipLaunchKernelGGL(attn_main_kernel<F16>, grid, block, 0, s, p);
-  hipLaunchKernelGGL(attn_repair_kernel<F16>, grid, block, 0, s, p);
   e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));

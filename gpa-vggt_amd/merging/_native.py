@@ -274,17 +274,16 @@ def _sim_argmax_fake(a, b):
 # gpa::attn_keybias
 # --------------------------------------------------------------------------
 
-@torch.library.custom_op("gpa::attn_keybias", mutates_args=())
-def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                 bias: Optional[torch.Tensor], sm_scale: float,
-                 return_lse: bool) -> Tuple[torch.Tensor, torch.Tensor]:
-    """softmax(q k^T * sm_scale + bias) v with a per-key bias.
+# Workspace layout of the attention (gpa_attn_keybias_workspace_bytes): per
+# (batch, head) one 144-byte record per 32-key tile, then 8 bytes of row
+# bounds per (batch, head), then one flag byte per 64-query wave (4 waves per
+# 256-query workgroup).
+_ATTN_TILE_KEYS, _ATTN_REC_BYTES, _ATTN_WG_QUERIES, _ATTN_WAVES = 32, 144, 256, 4
 
-    q [B,H,M,64], k/v [B,H,N,64], all bf16 or all fp16; bias broadcastable
-    to [B,H,1,N] (fp32, bf16 or fp16) or None.  Returns o [B,H,M,64] in q's
-    dtype and, if return_lse, the log2 log-sum-exp [B,H,M] fp32 (else an
-    empty tensor).
-    """
+
+def _attn_run(q, k, v, bias, sm_scale, return_lse):
+    """Validate, allocate and launch gpa_attn_keybias_{bf16,f16}; returns
+    (o, lse, workspace) with the workspace as the kernel left it."""
     tensors = [q, k, v] + ([bias] if bias is not None else [])
     dev = _require_gpu(*tensors)
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -322,7 +321,7 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lse = (torch.empty(B, H, M, device=dev, dtype=torch.float32) if return_lse
            else torch.empty(0, device=dev, dtype=torch.float32))
     if B == 0 or H == 0 or M == 0:
-        return o, lse
+        return o, lse, None
     L = lib()
     ws_bytes = L.gpa_attn_keybias_workspace_bytes(B, H, M, N)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
@@ -339,7 +338,43 @@ def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             _st(lse, 0) if return_lse else 0, _st(lse, 1) if return_lse else 0,
             ws.data_ptr(), ws_bytes, float(sm_scale), _stream(dev))
     _check(rc, "gpa::attn_keybias")
+    return o, lse, ws
+
+
+@torch.library.custom_op("gpa::attn_keybias", mutates_args=())
+def attn_keybias(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                 bias: Optional[torch.Tensor], sm_scale: float,
+                 return_lse: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """softmax(q k^T * sm_scale + bias) v with a per-key bias.
+
+    q [B,H,M,64], k/v [B,H,N,64], all bf16 or all fp16; bias broadcastable
+    to [B,H,1,N] (fp32, bf16 or fp16) or None.  Returns o [B,H,M,64] in q's
+    dtype and, if return_lse, the log2 log-sum-exp [B,H,M] fp32 (else an
+    empty tensor).
+    """
+    o, lse, _ = _attn_run(q, k, v, bias, sm_scale, return_lse)
     return o, lse
+
+
+def attn_keybias_offset_flags(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              bias: Optional[torch.Tensor], sm_scale: float,
+                              return_lse: bool = False):
+    """The attention plus which softmax offset each wave used (diagnostic).
+
+    Returns (o, lse, flags) with flags [B*H, ceil(M/256), 4] uint8: 1 where
+    the wave of 64 queries could not certify the fixed offset and ran the
+    lazily moved one, 0 where it kept the fixed offset (or holds no query).
+    """
+    o, lse, ws = _attn_run(q, k, v, bias, sm_scale, return_lse)
+    B, H, M, _ = q.shape
+    N = k.shape[2]
+    if ws is None:
+        return o, lse, torch.zeros(0, 0, _ATTN_WAVES, dtype=torch.uint8)
+    ntiles = -(-N // _ATTN_TILE_KEYS)
+    gx = -(-M // _ATTN_WG_QUERIES)
+    start = B * H * ntiles * _ATTN_REC_BYTES + B * H * 8
+    flags = ws[start:start + B * H * gx * _ATTN_WAVES].view(B * H, gx, _ATTN_WAVES)
+    return o, lse, flags
 
 
 @attn_keybias.register_fake

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import gpa_workloads as W
+from merging import _native
 from merging.fused_attention import attention_keybias
 from oracle.attention import attention_reference, lse_combine
 
@@ -99,28 +100,38 @@ def test_increasing_logits_force_rescales(dev):
 
 
 @pytest.mark.parametrize("lse", [False, True])
-def test_fixed_and_repaired_rows_mix(dev, lse):
-    """Rows whose score bound |q| max|k| sits far above their scores go
-    through the repair pass (lazily moved offset); their neighbours in the
-    same workgroup keep the fixed offset.  Both must match the reference."""
+def test_fixed_and_lazy_offset_waves_mix(dev, lse):
+    """Rows whose score bound |q| max|k| sits far above their scores (more
+    than the 160 log2 units the fixed offset covers) make their wave run the
+    lazily moved offset; the other waves of the same workgroups keep the
+    fixed one.  Both must match the reference, and the flags say which wave
+    ran which."""
     g = torch.Generator().manual_seed(11)
     M, N = 600, 1000
     q = torch.randn(1, 2, M, 64, generator=g) * 0.3
     k = torch.randn(1, 2, N, 64, generator=g) * 0.3
     k[:, :, :32] *= -1.0                              # tile 0 scores low for the boosted rows
     boost = torch.zeros(M, dtype=torch.bool)
-    boost[32:64] = True                               # one whole wave of workgroup 0
+    boost[32:64] = True                               # one whole block of wave 0, workgroup 0
     boost[[5, 300, 555]] = True                       # single rows inside other waves
-    q[:, :, boost] = k[:, :, 40:41].expand(-1, -1, int(boost.sum()), -1) * 100.0
+    q[:, :, boost] = k[:, :, 40:41].expand(-1, -1, int(boost.sum()), -1) * 300.0
     q, k = q.bfloat16(), k.bfloat16()
     v = torch.randn(1, 2, N, 64, generator=g).bfloat16()
     bias = torch.randn(1, 1, 1, N, generator=g)
-    o, l = attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125, True) \
-        if lse else (attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125), None)
+    o, l, flags = _native.attn_keybias_offset_flags(q.to(dev), k.to(dev), v.to(dev), bias.to(dev),
+                                                    0.125, lse)
     ref, ref_lse = attention_reference(q, k, v, bias, 0.125)
     _check(o, ref)
     if lse:
         assert (l.cpu() - ref_lse).abs().max().item() < LSE_TOL
+    want = torch.zeros(2, 3, 4, dtype=torch.uint8)
+    want[:, 0, 0] = 1                                 # rows 5, 32-63
+    want[:, 1, 0] = 1                                 # row 300 (256 + 44)
+    want[:, 2, 0] = 1                                 # row 555 (512 + 43)
+    assert torch.equal(flags.cpu(), want)
+    # the same call through the op agrees bit for bit
+    o2 = attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125)
+    assert torch.equal(o2, o)
 
 
 def test_replication_identity(dev):
@@ -214,3 +225,39 @@ def test_full_size_attention_workload(dev):
     err = (o[:, :, rows.to(dev)].float().cpu() - ref).abs()
     print(f"\n[attn c3] sample max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e}")
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+
+
+def test_full_size_sharp_logits_mix_offsets(dev):
+    """The 274,800 x 68,700 x 16-head workload (1,074 workgroups per head)
+    with sharp rows: every query of every fifth wave points along a planted
+    key of norm 40 in a late tile (key 60,000), so its logit for that key is
+    ~290 log2 units and its score bound sits ~290 above tile 0's scores --
+    those waves run the lazily moved offset, all others the fixed one.
+    Checked on a sample of both kinds of rows against the oracle."""
+    q, k, v, bias = W.attn_inputs(device=dev)
+    H, M, N = q.shape[1], q.shape[2], k.shape[2]
+    g = torch.Generator(device=dev).manual_seed(21)
+    kp = torch.randn(1, H, 1, 64, generator=g, device=dev)
+    kp = kp / kp.norm(dim=-1, keepdim=True)
+    k[:, :, 60_000] = (kp[:, :, 0] * 40.0).bfloat16()
+    wave_of = torch.arange(M, device=dev) // 64
+    sharp = wave_of % 5 == 0
+    q[:, :, sharp] = (kp * 40.0).bfloat16().expand(1, H, int(sharp.sum()), 64)
+    o, _, flags = _native.attn_keybias_offset_flags(q, k, v, bias, 0.125)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    waves = flags.view(H, -1)[:, :-(-M // 64)]       # [H, waves holding queries]
+    want = (torch.arange(waves.shape[1], device=dev) % 5 == 0).to(torch.uint8)
+    lazy_share = waves.float().mean().item()
+    print(f"\n[attn c3 sharp] {100 * lazy_share:.1f} % of waves on the lazy offset", flush=True)
+    assert torch.equal(waves, want.expand_as(waves))
+    cpu = torch.Generator().manual_seed(22)
+    rows = torch.cat([torch.nonzero(sharp).view(-1).cpu()[torch.randperm(int(sharp.sum()),
+                                                                          generator=cpu)[:48]],
+                      torch.nonzero(~sharp).view(-1).cpu()[torch.randperm(int((~sharp).sum()),
+                                                                           generator=cpu)[:48]]])
+    ref, _ = attention_reference(q[:, :, rows.to(dev)].cpu(), k.cpu(), v.cpu(), bias.cpu(), 0.125)
+    err = (o[:, :, rows.to(dev)].float().cpu() - ref).abs()
+    print(f"[attn c3 sharp] sample max-abs {err.max().item():.3e} mean-abs "
+          f"{err.mean().item():.3e}", flush=True)
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= 2e-3

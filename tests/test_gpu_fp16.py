@@ -15,8 +15,9 @@ bars (max-abs 2e-2, mean-abs 5e-3); and, since P is rounded to fp16 (11
 significant bits) instead of bf16 (8), an error well below the bf16
 kernel's on inputs both formats hold exactly -- which a path that silently
 ran bf16 would not show.  The log2 LSE sums fp16-rounded probabilities:
-within 2^-10 / ln 2 of the fp32 one.  Edge cases: rows routed to the repair
-pass, logits that raise the row max on every tile (lazy rescale at 2^15), a
+within 2^-10 / ln 2 of the fp32 one.  Edge cases: waves routed to the
+lazily moved offset, logits that raise the row max on every tile (lazy
+rescale at 2^15), a
 row whose max meets the score bound (largest P = 2^15, no overflow), an
 fp16 bias, the fp32-input cast under fp16 autocast.
 """
@@ -24,6 +25,7 @@ import numpy as np
 import pytest
 import torch
 
+from merging import _native
 from merging.fused_attention import attention_keybias
 from merging.fused_similarity import fused_similarity_argmax
 from oracle.attention import attention_reference
@@ -132,9 +134,10 @@ def test_attention_f16_matches_reference_and_beats_bf16(dev, B, H, M, N, with_bi
 
 
 @pytest.mark.parametrize("lse", [False, True])
-def test_attention_f16_fixed_and_repaired_rows_mix(dev, lse):
-    """Rows whose score bound sits far above their scores take the repair
-    pass; with fp16's 16-unit certification window more rows do."""
+def test_attention_f16_fixed_and_lazy_offset_waves_mix(dev, lse):
+    """Rows whose score bound sits far above their scores make their wave
+    run the lazily moved offset; with fp16's 16-unit certification window
+    more rows do.  The flags name the waves."""
     g = torch.Generator().manual_seed(11)
     M, N = 600, 1000
     q = torch.randn(1, 2, M, 64, generator=g) * 0.3
@@ -154,11 +157,17 @@ def test_attention_f16_fixed_and_repaired_rows_mix(dev, lse):
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
     if lse:
         assert (out[1].cpu() - ref_lse).abs().max().item() < LSE_TOL16
+    _, _, flags = _native.attn_keybias_offset_flags(
+        q.to(dev, torch.float16), k.to(dev, torch.float16), v.to(dev, torch.float16),
+        bias.to(dev, torch.float16), 0.125)
+    for wg, row in ((0, 32), (1, 300 - 256), (2, 555 - 512)):       # the boosted rows' waves
+        assert (flags[:, wg, row // 64] == 1).all()
 
 
 def test_attention_f16_increasing_logits_rescale(dev):
     """Each tile raises the row max (logits over ~46 log2 units): the bound is
-    far above tile 0, so the repair pass rescales at 2^15 on every tile."""
+    far above tile 0, so the wave runs the lazily moved offset and rescales
+    whenever a tile's max passes m + 15."""
     g = torch.Generator().manual_seed(4)
     n = 1024
     q = torch.ones(1, 1, 64, 64)
