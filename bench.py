@@ -7,11 +7,14 @@ workload (16 heads, 274,800 queries, 68,700 merged keys, head_dim 64), both
 on synthetic inputs already resident in HBM.  `value` is the step's
 algorithmic TFLOP/s (2*M*N*D for the similarity, 4*BH*M*N*D for attention).
 The JSON line also carries per-kernel ms / TFLOP/s / % of the bf16 dense
-MFMA peak, the reference 200-frame shapes, the end-to-end latency of one GPA
-block (100 frames) and of the whole GPA aggregator (200 frames) on the
-random-init VGGT-1B harness, the roofline of the dominant kernel and a CPU
-baseline (the torch restatement of the reference path, timed on a bounded
-sample on this host).
+MFMA peak (the reference 200-frame shapes, the unprojected 1024-d
+similarity, the frame-special calls, the HBM-bound kernels around the path,
+the fp16 twins, and sharp-logit attention with the share of waves on the
+lazily moved softmax offset), the end-to-end latency of one GPA block (100
+frames) and of the whole aggregator (200 frames) on the random-init VGGT-1B
+harness for the GPA schedule and for vanilla VGGT, the roofline of the
+dominant kernel and a CPU baseline (the torch restatement of the reference
+path, timed on a bounded sample on this host).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -119,6 +122,23 @@ def e2e_latency(dev) -> dict:
         log(f"[bench] aggregator 200 frames ({tag}): {ms:.1f} ms")
         del m
         torch.cuda.empty_cache()
+    # Vanilla VGGT on the same harness and images (eval_co3d.py:127-128: no
+    # merging, no frame-special blocks): every global block attends over all
+    # 274,800 tokens.  ~7 s per forward, so 1 warm-up call and the mean of 2.
+    vcfg = A.vanilla_config()
+    vm = A.build_aggregator(vcfg, device=dev)
+    ms, peak = A.timed(run(lambda: vm(imgs)), warmup=1, iters=2)
+    flops = A.aggregator_flops(vcfg, frames)
+    gpa_ms = res["aggregator_200f_reference_defaults"]["ms"]
+    res["aggregator_200f_vanilla"] = {
+        "ms": round(ms, 1), "peak_gib": round(peak, 2),
+        "tflop": {k: round(v / 1e12, 2) for k, v in flops.items()},
+        "protocol": "1 warm-up call, mean of 2",
+        "gpa_speedup": round(ms / gpa_ms, 3),
+        "reference_speedup": "2.58x at 200 frames (README.md:21, reference hardware not stated)"}
+    log(f"[bench] aggregator 200 frames (vanilla): {ms:.1f} ms, GPA speed-up {ms / gpa_ms:.2f}x")
+    del vm, imgs
+    torch.cuda.empty_cache()
     return res
 
 
@@ -359,6 +379,34 @@ def main(argv=None) -> int:
             "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
             "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
         del metric, order
+        # The fused qk LayerNorm + 2D RoPE + cast of every aggregator block
+        # (vggt/layers/attention.py:210-220) at 200 frames: the bf16 QKV
+        # projection [1, 274800, 3072] in, q and k [1, 16, 274800, 64] out
+        # (bf16, and fp32 k as the merged blocks keep it for the K merge).
+        import gpa_aggregator as A
+        qkv = (torch.randn(1, S * P, 3 * 1024, device=dev)).bfloat16()
+        ln_w = torch.ones(2, 64, device=dev)
+        ln_b = torch.zeros(2, 64, device=dev)
+        rope = A.Rope2D(100.0).table(A.frame_positions(37, pts, dev), 64)
+        for k_f32, tag in ((False, "bf16"), (True, "k_f32")):
+            fn = lambda: torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, rope.pos, rope.cs,  # noqa: E731
+                                                    16, False, k_f32)
+            fn()
+            t = statistics.median(event_ms(fn, 5))
+            nbytes = S * P * (2 * 1024 * 2 + 1024 * 2 + 1024 * (4 if k_f32 else 2))
+            kernels[f"qk_norm_rope_200f_274800x16h_{tag}"] = {
+                "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+                "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+        del qkv
+        # The unprojected metric (metric_dim=0, D = 1024) at the 200-frame
+        # shape: the GEMM-tiled similarity kernel.
+        s3, d3 = W.sim_inputs(m=207_955, n=66_845, out_dim=1024, seed=4, device=dev)
+        fn = lambda: fused_similarity_argmax(s3, d3)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 3))
+        kernels["sim_argmax_200f_207955x66845x1024"] = kernel_entry(
+            W.sim_flops(1, 207_955, 66_845, 1024), t)
+        del s3, d3
         log("[bench] 200-frame shapes done")
 
     if not args.no_200f:
@@ -377,6 +425,28 @@ def main(argv=None) -> int:
         kernels["attn_keybias_f16_16h_274800x68700"] = kernel_entry(f_attn, t)
         del qh, kh, vh, bh
         log("[bench] fp16 shapes done")
+        # Sharp logits: q and k scaled up so the Cauchy-Schwarz score bound
+        # sits far above the rows' real scores and waves fall back from the
+        # certified fixed softmax offset to the lazily moved one (same
+        # workload otherwise).  lazy_waves_pct is read from the kernel's
+        # per-wave flags.
+        for dt, scale in ((torch.bfloat16, 40.0), (torch.float16, 6.0), (torch.float16, 12.0)):
+            qs, ks = (q.float() * scale).to(dt), (k.float() * scale).to(dt)
+            vs, bs = v.to(dt), bias.to(dt)
+            _, _, flags = _native.attn_keybias_offset_flags(qs, ks, vs, bs, SM_SCALE)
+            lazy = float(flags.float().mean().item())
+            fn = lambda: attention_keybias(qs, ks, vs, bs, SM_SCALE)  # noqa: E731
+            fn()
+            t = statistics.median(event_ms(fn, 3))
+            tag = "bf16" if dt == torch.bfloat16 else "f16"
+            entry = kernel_entry(f_attn, t)
+            base = attn_ms if dt == torch.bfloat16 else \
+                kernels["attn_keybias_f16_16h_274800x68700"]["ms"]
+            entry.update({"qk_scale": scale, "lazy_waves_pct": round(100 * lazy, 2),
+                          "vs_certified": round(t / base, 3)})
+            kernels[f"attn_keybias_sharp_{tag}_x{int(scale)}_16h_274800x68700"] = entry
+            del qs, ks, vs, bs, flags
+        log("[bench] sharp-logit shapes done")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12
     traffic = None
