@@ -1,12 +1,15 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|attn|own|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|sharp|own|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
          (not in `all`)
+  sim1024 the unprojected 1024-d similarity at the 200-frame shape (not in `all`)
   attn   biased attention, 16 heads x 274,800 queries x 68,700 keys x 64
+  sharp  the attention workload with q and k scaled by 40: every wave falls back
+         to the lazily moved softmax offset (not in `all`)
   own    own-frame attention of the frame-special split, 3,200 (frame, head)
          pairs x 1,374 queries x 1,369 keys, no bias, with LSE (not in `all`)
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
@@ -42,8 +45,8 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "sim200", "attn", "own", "merge", "front", "pool", "sim16", "attn16", "attn0", "copy",
-                     "all"):
+    if which not in ("sim", "sim200", "sim1024", "attn", "sharp", "own", "merge", "front", "pool",
+                     "sim16", "attn16", "attn0", "copy", "all"):
         print(__doc__, file=sys.stderr)
         return 2
 
@@ -76,6 +79,21 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"sim200 207955x66845x128 x {reps} done", flush=True)
         del s, d
+    if which == "sim1024":
+        s, d = W.sim_inputs(m=207_955, n=66_845, out_dim=1024, seed=4, device=dev)
+        for _ in range(reps):
+            fused_similarity_argmax(s, d)
+        torch.cuda.synchronize()
+        print(f"sim1024 207955x66845x1024 x {reps} done", flush=True)
+        del s, d
+    if which == "sharp":
+        q, k, v, b = W.attn_inputs(device=dev)
+        q, k = (q.float() * 40).bfloat16(), (k.float() * 40).bfloat16()
+        for _ in range(reps):
+            attention_keybias(q, k, v, b, 0.125)
+        torch.cuda.synchronize()
+        print(f"sharp 16x274800x68700x64 (q, k x 40) x {reps} done", flush=True)
+        del q, k, v, b
     if which in ("merge", "all"):
         t, off, tok = W.merge_inputs(device=dev)
         for _ in range(reps):
