@@ -355,7 +355,7 @@ def main(argv=None) -> int:
         # Row f2: the pooled shared set (kp 8: 25 seeds per frame) at 200 frames.
         kk = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
         vv = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
-        fn = lambda: torch.ops.gpa.pool_shared(kk, vv, S, pts, 37, 8, False)  # noqa: E731
+        fn = lambda: torch.ops.gpa.pool_shared(kk, vv, S, pts, 37, 37, 8, False)  # noqa: E731
         fn()
         t = statistics.median(event_ms(fn, 5))
         nbytes = 2 * 16 * S * (P - pts) * 64 * 2

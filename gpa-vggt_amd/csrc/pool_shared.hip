@@ -1,8 +1,10 @@
 // Content-adaptive pooled summaries of the frame-special shared K/V set.
 //
 // For every (batch b, head h, frame s) group of the frame's patch keys
-// x_p = k[b, h, s*P + pts + p, :] (p < grid*grid, head dim 64):
-//   seeds   y_g = x at the stride-kp lattice patches (gy*kp, gx*kp)
+// x_p = k[b, h, s*P + pts + p, :] (p < gh*gw on a gh x gw patch grid, head
+// dim 64):
+//   seeds   y_g = x at the stride-kp lattice patches (gy*kp, gx*kp),
+//           g = gy*nw + gx, nh = ceil(gh/kp), nw = ceil(gw/kp)
 //   assign  a_p = argmax_g bf16( bf16(x_p / max(|x_p|, 1e-6)) . bf16(y_g / max(|y_g|, 1e-6)) )
 //           (fp32 dot products rounded to bf16, lowest g on ties)
 //   size    n_g = #{p : a_p = g}
@@ -14,22 +16,27 @@
 // its scores come back in bf16, argmax takes the first maximum, and the
 // sums run in fp32 (scatter_add_, :132-139) before the cast back.  The
 // reference sums with atomics in a run-dependent order; here every sum has
-// a single owner and a fixed order, so the means are deterministic.
+// a fixed order, so the means are deterministic.
 //
-// One workgroup (4 waves) per group; both steps run on MFMA
-// (v_mfma_f32_32x32x16_bf16).
-//   Assignment: the normalised seeds are the A operands (one or two blocks
-//   of 32 seeds, held in registers), each 32-row tile of normalised patch
-//   keys the B operand; a lane's 16 scores of a row are rounded to bf16 and
-//   reduced with the partner lane (lowest seed on ties).  The assignment
-//   bytes go to LDS.
-//   Sums: a one-hot GEMM, D[seed][feature] = sum_rows [a_row == seed] x,
-//   exact bf16 products summed in fp32.  Wave w owns one tensor (K or V) and
-//   one feature half over every tile: its raw rows are staged in an LDS tile
-//   and read back transposed as the B operand (rows along k), the A operand
-//   is built from the assignment bytes, and the means go straight from the
-//   accumulators to the output.
-// HBM-bound: K read twice (the second pass mostly from L2), V once.
+// One workgroup (4 waves) per group; wave w takes the 32-row tiles
+// t = w, w+4, ... of the frame, first of K (assignment and K sums), then of
+// V (V sums), so each K and V row is read from memory once.
+//   Assignment: the normalised seeds are the A operands of
+//   v_mfma_f32_32x32x16_bf16 (one or two blocks of 32 seeds, held in
+//   registers), the tile's normalised keys the B operand; a lane's 16 scores
+//   of a row are rounded to bf16 and reduced with the partner lane (lowest
+//   seed on ties).  The assignment bytes go to LDS, the counts to LDS
+//   counters.
+//   Sums, in the same iteration: a one-hot GEMM per feature half,
+//   D[seed][feature] += sum_rows [a_row == seed] x[row][feature], exact bf16
+//   products summed in fp32.  The tile's raw rows (already in registers for
+//   the assignment) are staged in the wave's LDS tile and read back
+//   transposed as the B operand (rows along k); the A operand is built from
+//   the assignment bytes.
+//   Each wave ends a sweep with partial sums over its tiles; the four
+//   partials meet in LDS and are added in wave order (fixed), then divided
+//   by the counts.
+// HBM-bound: every K and V row read once.
 #include "gpa_common.h"
 
 #include <math.h>
@@ -51,20 +58,28 @@ struct PoolArgs {
   float* size;
   int32_t* assign;   // nullable
   int64_t k_sb, k_sh, k_sn, v_sb, v_sh, v_sn;
-  int H, S, P, pts, grid, kp, nh, npool;
+  int H, S, P, pts, gh, gw, kp, nw, npool;
 };
-
-__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
 // Row stride of a wave's staged tile (32 rows x 32 features), in bf16: 8 of
 // padding, so the transposed reads (lanes = features, the two lane halves 8
 // rows apart) fall in different banks.
 constexpr int kStage = 32 + 8;
+// Row stride of the partial-sum buffer (32 features + 1 of padding).
+constexpr int kRed = 33;
 
-__global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
+
+// NSB: blocks of 32 seeds (1 or 2), so the accumulators of an absent block
+// take no registers.  One block fits three waves per SIMD without spills
+// (158 VGPRs), 8 % faster than two; two blocks stay at two (spills at three).
+template <int NSB>
+__global__ __launch_bounds__(kPoolThreads) __attribute__((amdgpu_waves_per_eu(NSB == 1 ? 3 : 1)))
+void pool_shared_kernel(PoolArgs a) {
   __shared__ int count[kMaxPool];
   __shared__ __attribute__((aligned(16))) uint8_t asg[kMaxPatches];
   __shared__ __attribute__((aligned(16))) uint16_t stage[kPoolWaves][32][kStage];
+  __shared__ float red[kPoolWaves][kMaxPool][kRed];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -72,7 +87,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
   const int s = grp % a.S;
   const int bh = grp / a.S;
   const int h = bh % a.H, b = bh / a.H;
-  const int npatch = a.grid * a.grid;
+  const int npatch = a.gh * a.gw;
   const uint16_t* K = a.k + b * a.k_sb + h * a.k_sh + ((int64_t)s * a.P + a.pts) * a.k_sn;
   const uint16_t* Vp = a.v + b * a.v_sb + h * a.v_sh + ((int64_t)s * a.P + a.pts) * a.v_sn;
 
@@ -101,15 +116,14 @@ __global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
 
   // Seed blocks: block sb holds seeds 32sb .. 32sb+31 in lane rows l32 (zero
   // past npool; their scores are masked anyway).
-  const int nsb = (a.npool + 31) / 32;
-  bf16x8 seed[2][4];
+  bf16x8 seed[NSB][4];
 #pragma unroll
-  for (int sb = 0; sb < 2; ++sb) {
+  for (int sb = 0; sb < NSB; ++sb) {
     const int g = sb * 32 + l32;
     const int gc = g < a.npool ? g : a.npool - 1;
-    const int gy = gc / a.nh, gx = gc % a.nh;
+    const int gy = gc / a.nw, gx = gc % a.nw;
     bf16x8 r[4];
-    load_half(K, a.k_sn, gy * a.kp * a.grid + gx * a.kp, r);
+    load_half(K, a.k_sn, gy * a.kp * a.gw + gx * a.kp, r);
     normalise(r, seed[sb]);
     if (g >= a.npool)
 #pragma unroll
@@ -117,19 +131,19 @@ __global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
   }
   __syncthreads();                             // counts cleared
 
+  uint16_t(&st)[32][kStage] = stage[wave];
   const int ntile = (npatch + 31) / 32;        // ntile * 32 <= kMaxPatches
-  // Assignment: every row's scores against the seeds, rounded to bf16.
-  for (int t = wave; t < ntile; t += kPoolWaves) {
-    const int p = t * 32 + l32;
-    const bool valid = p < npatch;
-    bf16x8 rk[4], xb[4];
-    load_half(K, a.k_sn, valid ? p : npatch - 1, rk);
+  const int64_t out_row0 = ((int64_t)bh * a.S + s) * a.npool;   // row of [B, H, S*npool]
+
+  // Score a tile's normalised rows against the seeds; the row's seed (lowest
+  // on ties) goes to asg, the count and the optional assignment output.
+  auto assign_tile = [&](int t, bool valid, const bf16x8 (&rk)[4]) {
+    bf16x8 xb[4];
     normalise(rk, xb);
     float best = -INFINITY;
     int bi = 0;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {           // compile-time index into seed[]
-      if (sb >= nsb) break;                    // wave-uniform
+    for (int sb = 0; sb < NSB; ++sb) {
       f32x16 sc = {};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) sc = mfma32x32x16(seed[sb][ks], xb[ks], sc);
@@ -147,83 +161,96 @@ __global__ __launch_bounds__(kPoolThreads) void pool_shared_kernel(PoolArgs a) {
     const int pi = __shfl_xor(bi, 32);
     if (pb > best || (pb == best && pi < bi)) bi = pi;
     if (hi == 0) {
+      const int p = t * 32 + l32;
       asg[p] = valid ? (uint8_t)bi : (uint8_t)0xff;   // 0xff matches no seed
       if (valid) {
         atomicAdd(&count[bi], 1);
         if (a.assign) a.assign[(int64_t)grp * npatch + p] = bi;
       }
     }
-  }
-  __syncthreads();
-
-  // Sums and means: wave w owns tensor (w >> 1 ? V : K) and feature half
-  // fb = w & 1 over every tile, accumulating the one-hot GEMM
-  //   D[seed][feature] = sum_rows [a_row == seed] x[row][feature]
-  // on MFMA (A = one-hot from the assignment bytes, B = the raw rows, staged
-  // in the wave's LDS tile and read back transposed so rows run along k).
-  // Each (seed, feature) has one owner, so the sums need no atomics and are
-  // deterministic.  The next tile's rows load while this one is multiplied.
-  const bool is_v = wave >> 1;
-  const int fb = wave & 1;
-  const uint16_t* X = is_v ? Vp : K;
-  const int64_t x_sn = is_v ? a.v_sn : a.k_sn;
-  auto load_quarter = [&](int t, bf16x8 (&r)[2]) {
-    const int p = t * 32 + l32;
-    const uint16_t* row = X + (int64_t)(p < npatch ? p : npatch - 1) * x_sn + 32 * fb + 16 * hi;
-    r[0] = *reinterpret_cast<const bf16x8*>(row);
-    r[1] = *reinterpret_cast<const bf16x8*>(row + 8);
   };
-  f32x16 acc[2] = {};
-  bf16x8 nx[2];
-  load_quarter(0, nx);
-  for (int t = 0; t < ntile; ++t) {
-    const bool valid = t * 32 + l32 < npatch;
-    *reinterpret_cast<bf16x8*>(&stage[wave][l32][16 * hi]) = valid ? nx[0] : bf16x8{};
-    *reinterpret_cast<bf16x8*>(&stage[wave][l32][16 * hi + 8]) = valid ? nx[1] : bf16x8{};
-    load_quarter(t + 1 < ntile ? t + 1 : t, nx);
-    // The wave's own LDS writes above are visible to these reads (in order).
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int r0 = 16 * kk + 8 * hi;         // rows r0 .. r0+7 of the tile
-      const uint2 ab = *reinterpret_cast<const uint2*>(&asg[t * 32 + r0]);
-      u32x4 bx;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bx[q] = (uint32_t)stage[wave][r0 + 2 * q][l32] |
-                ((uint32_t)stage[wave][r0 + 2 * q + 1][l32] << 16);
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        if (sb >= nsb) break;                  // wave-uniform
-        const uint32_t id = (uint32_t)(sb * 32 + l32);
-        u32x4 oh;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t w = q < 2 ? ab.x : ab.y;
-          const uint32_t b0 = (w >> (16 * (q & 1))) & 0xffu, b1 = (w >> (16 * (q & 1) + 8)) & 0xffu;
-          oh[q] = (b0 == id ? 0x3f80u : 0u) | (b1 == id ? 0x3f800000u : 0u);   // bf16 1.0
-        }
-        acc[sb] = mfma32x32x16(__builtin_bit_cast(bf16x8, oh), __builtin_bit_cast(bf16x8, bx),
-                               acc[sb]);
-      }
-    }
-  }
 
-  // Means straight to the output (counts are complete since the barrier).
-  const int64_t out_row0 = ((int64_t)bh * a.S + s) * a.npool;   // row of [B, H, S*npool]
-  uint16_t* out = is_v ? a.pv : a.pk;
+  // One-hot sums of a tile into acc[feature half][seed block].  The rows are
+  // staged in the wave's LDS tile and read back transposed (rows along k);
+  // the wave's own LDS writes and reads execute in order, so no barrier is
+  // needed between the staging and the reads, nor before the next staging.
+  auto sum_tile = [&](int t, bool valid, const bf16x8 (&rx)[4], f32x16 (&acc)[2][NSB]) {
 #pragma unroll
-  for (int sb = 0; sb < 2; ++sb) {
-    if (sb >= nsb) break;
+    for (int fh = 0; fh < 2; ++fh) {
+      // Features 32fh .. 32fh+31: this lane holds 16ks + 8hi .. +8 of
+      // ks = 2fh and 2fh+1.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int g = sb * 32 + mfma_row(r, hi);
-      if (g < a.npool) {
-        const float inv = 1.0f / fmaxf((float)count[g], 1.0f);
-        out[(out_row0 + g) * kPoolD + 32 * fb + l32] =
-            __builtin_bit_cast(uint16_t, (__bf16)(acc[sb][r] * inv));
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<bf16x8*>(&st[l32][16 * c + 8 * hi]) = valid ? rx[2 * fh + c] : bf16x8{};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int r0 = 16 * kk + 8 * hi;       // rows r0 .. r0+7 of the tile
+        const uint2 ab = *reinterpret_cast<const uint2*>(&asg[t * 32 + r0]);
+        u32x4 bx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bx[q] = (uint32_t)st[r0 + 2 * q][l32] | ((uint32_t)st[r0 + 2 * q + 1][l32] << 16);
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          const uint32_t id = (uint32_t)(sb * 32 + l32);
+          u32x4 oh;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t w = q < 2 ? ab.x : ab.y;
+            const uint32_t b0 = (w >> (16 * (q & 1))) & 0xffu, b1 = (w >> (16 * (q & 1) + 8)) & 0xffu;
+            oh[q] = (b0 == id ? 0x3f80u : 0u) | (b1 == id ? 0x3f800000u : 0u);   // bf16 1.0
+          }
+          acc[fh][sb] = mfma32x32x16(__builtin_bit_cast(bf16x8, oh), __builtin_bit_cast(bf16x8, bx),
+                                     acc[fh][sb]);
+        }
       }
     }
-  }
+  };
+
+  // The four waves' partial sums meet in LDS, one feature half at a time,
+  // and are added in wave order; the means go straight to the output.
+  auto reduce_store = [&](f32x16 (&acc)[2][NSB], uint16_t* out) {
+#pragma unroll
+    for (int fh = 0; fh < 2; ++fh) {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave][sb * 32 + mfma_row(r, hi)][l32] = acc[fh][sb][r];
+      __syncthreads();
+      for (int e = tid; e < a.npool * 32; e += kPoolThreads) {
+        const int g = e >> 5, f = e & 31;
+        const float sum = ((red[0][g][f] + red[1][g][f]) + red[2][g][f]) + red[3][g][f];
+        const float inv = 1.0f / fmaxf((float)count[g], 1.0f);
+        out[(out_row0 + g) * kPoolD + 32 * fh + f] = __builtin_bit_cast(uint16_t, (__bf16)(sum * inv));
+      }
+      __syncthreads();
+    }
+  };
+
+  // Wave w takes tiles w, w+4, ...; the next tile's rows load while this
+  // one is processed.  Sweep 1 over K: assignment and K sums; sweep 2 over
+  // V: V sums with the assignment of the same wave's tiles.  Each row of K
+  // and V is read once.
+  auto sweep = [&](const uint16_t* X, int64_t x_sn, bool with_assign, uint16_t* out) {
+    f32x16 acc[2][NSB] = {};
+    bf16x8 nx[4];
+    const int p0 = wave * 32 + l32;
+    load_half(X, x_sn, p0 < npatch ? p0 : npatch - 1, nx);
+    for (int t = wave; t < ntile; t += kPoolWaves) {
+      const int p = t * 32 + l32;
+      const bool valid = p < npatch;
+      bf16x8 rx[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) rx[ks] = nx[ks];
+      const int pn = p + 32 * kPoolWaves;
+      load_half(X, x_sn, pn < npatch ? pn : npatch - 1, nx);
+      if (with_assign) assign_tile(t, valid, rx);
+      sum_tile(t, valid, rx, acc);
+    }
+    reduce_store(acc, out);                    // the first barrier completes the counts
+  };
+  sweep(K, a.k_sn, true, a.pk);
+  sweep(Vp, a.v_sn, false, a.pv);
   for (int g = tid; g < a.npool; g += kPoolThreads) a.size[out_row0 + g] = (float)count[g];
 }
 
@@ -234,11 +261,12 @@ using namespace gpa;
 
 extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* pooled_v,
                                     float* size, int32_t* assign, int64_t B, int64_t H,
-                                    int64_t S, int64_t P, int64_t pts, int64_t grid, int64_t kp,
-                                    int64_t D, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                                    int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream) {
+                                    int64_t S, int64_t P, int64_t pts, int64_t grid_h,
+                                    int64_t grid_w, int64_t kp, int64_t D, int64_t k_sb,
+                                    int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh,
+                                    int64_t v_sn, void* stream) {
   gpa_clear_error();
-  if (B < 0 || H < 0 || S < 0 || P < 0 || pts < 0 || grid < 0 || kp <= 0) {
+  if (B < 0 || H < 0 || S < 0 || P < 0 || pts < 0 || grid_h < 0 || grid_w < 0 || kp <= 0) {
     gpa_set_error("gpa_pool_shared_bf16: negative size or kp <= 0");
     return GPA_E_INVALID;
   }
@@ -246,21 +274,21 @@ extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k
     gpa_set_error("gpa_pool_shared_bf16: head dim %lld unsupported (64 only)", (long long)D);
     return GPA_E_UNSUPPORTED;
   }
-  if (B == 0 || H == 0 || S == 0 || grid == 0) return GPA_OK;
+  if (B == 0 || H == 0 || S == 0 || grid_h == 0 || grid_w == 0) return GPA_OK;
   if (!k || !v || !pooled_k || !pooled_v || !size) {
     gpa_set_error("gpa_pool_shared_bf16: null pointer");
     return GPA_E_INVALID;
   }
-  if (P < pts + grid * grid) {
+  if (P < pts + grid_h * grid_w) {
     gpa_set_error("gpa_pool_shared_bf16: frame of %lld tokens cannot hold %lld specials and a "
-                  "%lldx%lld patch grid", (long long)P, (long long)pts, (long long)grid,
-                  (long long)grid);
+                  "%lldx%lld patch grid", (long long)P, (long long)pts, (long long)grid_h,
+                  (long long)grid_w);
     return GPA_E_INVALID;
   }
-  const int64_t nh = (grid + kp - 1) / kp;
-  if (nh * nh > kMaxPool || grid * grid > kMaxPatches) {
+  const int64_t nh = (grid_h + kp - 1) / kp, nw = (grid_w + kp - 1) / kp;
+  if (nh * nw > kMaxPool || grid_h * grid_w > kMaxPatches) {
     gpa_set_error("gpa_pool_shared_bf16: %lld seeds / %lld patches exceed the kernel's 64 / 4096",
-                  (long long)(nh * nh), (long long)(grid * grid));
+                  (long long)(nh * nw), (long long)(grid_h * grid_w));
     return GPA_E_UNSUPPORTED;
   }
   const bool aligned = (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 &&
@@ -286,10 +314,15 @@ extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k
   a.assign = assign;
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_sn = k_sn;
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
-  a.H = (int)H; a.S = (int)S; a.P = (int)P; a.pts = (int)pts; a.grid = (int)grid;
-  a.kp = (int)kp; a.nh = (int)nh; a.npool = (int)(nh * nh);
-  hipLaunchKernelGGL(pool_shared_kernel, dim3((unsigned)groups), dim3(kPoolThreads), 0,
-                     (hipStream_t)stream, a);
+  a.H = (int)H; a.S = (int)S; a.P = (int)P; a.pts = (int)pts;
+  a.gh = (int)grid_h; a.gw = (int)grid_w;
+  a.kp = (int)kp; a.nw = (int)nw; a.npool = (int)(nh * nw);
+  if (a.npool > 32)
+    hipLaunchKernelGGL(pool_shared_kernel<2>, dim3((unsigned)groups), dim3(kPoolThreads), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(pool_shared_kernel<1>, dim3((unsigned)groups), dim3(kPoolThreads), 0,
+                       (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     gpa_set_error("gpa_pool_shared_bf16: launch failed: %s", hipGetErrorString(e));

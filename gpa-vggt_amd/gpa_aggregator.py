@@ -301,7 +301,7 @@ class GpaAttention(nn.Module):
         out_a, lse_a = attention_keybias(q_f, own_k, own_v, None, self.scale, return_lse=True)
         del own_k, own_v
         if kp > 0:
-            pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, g, kp)
+            pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, g, g, kp)
             if self.merge_log is not None:
                 self.merge_log.append({"kind": "pool", "frames": S, "pool_size": pool_size})
             sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
@@ -321,53 +321,56 @@ class GpaAttention(nn.Module):
 POOL_KERNEL_MAX_SEEDS = 64      # seeds per frame the gpa::pool_shared kernel holds
 
 
-def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: int, kp: int,
-                    want_assign: bool = False):
+def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid_h: int,
+                    grid_w: int, kp: int, want_assign: bool = False):
     """The pooled summaries of the shared set (attention.py:113-140) from
-    k, v [B, H, S*P, D]: the `gpa::pool_shared` kernel for up to 64 seeds per
-    frame (pool stride >= 5 at grid 37, the reference default 8 included);
-    above that (stride <= 4) the reference's own torch ops on the device
-    (`pool_shared_torch`).  Returns (pooled_k, pooled_v [B, H, S*npool, D],
-    size [B, H, S, npool] fp32, assign [B, H, S, grid*grid] or an empty tensor)."""
-    nh = -(-grid // kp)
-    if nh * nh <= POOL_KERNEL_MAX_SEEDS and k.dtype == torch.bfloat16:
-        return torch.ops.gpa.pool_shared(k, v, frames, pts, grid, kp, want_assign)
+    k, v [B, H, S*P, D] on a grid_h x grid_w patch grid (ph x pw there): the
+    `gpa::pool_shared` kernel for up to 64 seeds per frame (pool stride >= 5
+    at grid 37, the reference default 8 included); above that (stride <= 4)
+    the reference's own torch ops on the device (`pool_shared_torch`).
+    Returns (pooled_k, pooled_v [B, H, S*npool, D], size [B, H, S, npool]
+    fp32, assign [B, H, S, grid_h*grid_w] or an empty tensor)."""
+    npool = -(-grid_h // kp) * -(-grid_w // kp)
+    if npool <= POOL_KERNEL_MAX_SEEDS and k.dtype == torch.bfloat16:
+        return torch.ops.gpa.pool_shared(k, v, frames, pts, grid_h, grid_w, kp, want_assign)
     B, H, N, D = k.shape
     P = N // frames
     pk, pv, size, assign = pool_shared_torch(k.view(B, H, frames, P, D),
-                                             v.view(B, H, frames, P, D), pts, grid, kp)
+                                             v.view(B, H, frames, P, D), pts, grid_h, grid_w, kp)
     return pk, pv, size, assign if want_assign else assign.new_empty(0)
 
 
-def pool_shared_torch(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid: int, kp: int):
+def pool_shared_torch(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid_h: int, grid_w: int,
+                      kp: int):
     """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140),
     restated with torch ops.  The harness runs the `gpa::pool_shared` kernel
     up to 64 seeds per frame and this restatement above that (pool stride
     <= 4 at grid 37); the tests pin the kernel against it.
 
-    k5/v5 [B, H, S, P, D].  Seeds are the stride-kp lattice patches; every
-    patch joins the seed whose key it matches best by cosine (per head), and
-    a summary is the mean of its group, for keys and values alike.  Returns
-    (pooled_k, pooled_v [B, H, S*npool, D] in the input dtype, size
-    [B, H, S, npool] fp32, assign [B, H, S, grid*grid] int64).
+    k5/v5 [B, H, S, P, D], patches row-major on a grid_h x grid_w grid.
+    Seeds are the stride-kp lattice patches; every patch joins the seed whose
+    key it matches best by cosine (per head), and a summary is the mean of
+    its group, for keys and values alike.  Returns (pooled_k, pooled_v
+    [B, H, S*npool, D] in the input dtype, size [B, H, S, npool] fp32,
+    assign [B, H, S, grid_h*grid_w] int64).
     """
     B, H, S, P, D = k5.shape
-    nh = -(-grid // kp)
-    npool = nh * nh
-    xk = k5[:, :, :, pts:].reshape(B, H, S, grid, grid, D)
+    npatch = grid_h * grid_w
+    npool = -(-grid_h // kp) * -(-grid_w // kp)
+    xk = k5[:, :, :, pts:].reshape(B, H, S, grid_h, grid_w, D)
     seeds = xk[:, :, :, ::kp, ::kp].reshape(B, H, S, npool, D).float()
-    a = xk.reshape(B, H, S, grid * grid, D).float()
+    a = xk.reshape(B, H, S, npatch, D).float()
     a = a / a.norm(dim=-1, keepdim=True).clamp_min(1e-6)
     seeds = seeds / seeds.norm(dim=-1, keepdim=True).clamp_min(1e-6)
     assign = torch.matmul(a, seeds.transpose(-1, -2).contiguous()).argmax(-1)
     del a, seeds
     size = torch.zeros(B, H, S, npool, device=k5.device, dtype=torch.float32)
     size.scatter_add_(3, assign, torch.ones_like(assign, dtype=torch.float32))
-    idx = assign[..., None].expand(B, H, S, grid * grid, D)
+    idx = assign[..., None].expand(B, H, S, npatch, D)
     out = []
     for t5 in (k5, v5):
         acc = torch.zeros(B, H, S, npool, D, device=k5.device, dtype=torch.float32)
-        acc.scatter_add_(3, idx, t5[:, :, :, pts:].reshape(B, H, S, grid * grid, D).float())
+        acc.scatter_add_(3, idx, t5[:, :, :, pts:].reshape(B, H, S, npatch, D).float())
         acc /= size.clamp_min(1.0).unsqueeze(-1)
         out.append(acc.reshape(B, H, S * npool, D).to(t5.dtype))
     return out[0], out[1], size, assign

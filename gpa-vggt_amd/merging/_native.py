@@ -16,9 +16,9 @@ two custom ops:
     gpa::qk_norm_rope(Tensor qkv, Tensor ln_w, Tensor ln_b, float eps,
                       Tensor? pos, Tensor? rope_cs, int heads, bool q_f32,
                       bool k_f32) -> (Tensor q, Tensor k)
-    gpa::pool_shared(Tensor k, Tensor v, int frames, int pts, int grid, int kp,
-                     bool want_assign) -> (Tensor pk, Tensor pv, Tensor size,
-                                           Tensor assign)
+    gpa::pool_shared(Tensor k, Tensor v, int frames, int pts, int grid_h,
+                     int grid_w, int kp, bool want_assign)
+                     -> (Tensor pk, Tensor pv, Tensor size, Tensor assign)
 
 All launch on torch's current stream of the input's device.  There is no
 fallback: a missing library or a non-GPU tensor raises.
@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -122,7 +122,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.gpa_pool_shared_bf16.restype = ctypes.c_int
     lib.gpa_pool_shared_bf16.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp,  # k, v, pooled_k, pooled_v, size, assign
-        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # B, H, S, P, pts, grid, kp, D
+        _i64, _i64, _i64, _i64, _i64,  # B, H, S, P, pts
+        _i64, _i64, _i64, _i64,        # grid_h, grid_w, kp, D
         _i64, _i64, _i64, _i64, _i64, _i64,  # k strides, v strides
         _vp,                           # stream
     ]
@@ -554,11 +555,14 @@ def _qk_norm_rope_fake(qkv, ln_w, ln_b, eps, pos, rope_cs, heads, q_f32, k_f32):
 
 
 @torch.library.custom_op("gpa::pool_shared", mutates_args=())
-def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: int, kp: int,
-                want_assign: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid_h: int,
+                grid_w: int, kp: int, want_assign: bool
+                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Pooled summaries of the frame-special shared set from k, v [B, H, S*P, 64]
-    (bf16): returns pooled k, v [B, H, S*npool, 64] bf16, size [B, H, S, npool]
-    fp32 and, if asked, the assignment [B, H, S, grid*grid] int32 (else empty)."""
+    (bf16) on a grid_h x grid_w patch grid: returns pooled k, v
+    [B, H, S*npool, 64] bf16, size [B, H, S, npool] fp32 and, if asked, the
+    assignment [B, H, S, grid_h*grid_w] int32 (else empty);
+    npool = ceil(grid_h/kp) * ceil(grid_w/kp)."""
     dev = _require_gpu(k, v)
     for name, t in (("k", k), ("v", v)):
         if t.dtype != torch.bfloat16 or t.dim() != 4:
@@ -566,13 +570,14 @@ def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: i
                              f"{tuple(t.shape)}")
     if k.shape != v.shape:
         raise ValueError(f"gpa::pool_shared: k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    if kp <= 0 or grid_h < 0 or grid_w < 0:
+        raise ValueError(f"gpa::pool_shared: grid {grid_h}x{grid_w}, kp {kp}")
     B, H, N, D = k.shape
     S = int(frames)
     if S <= 0 or N % S != 0:
         raise ValueError(f"gpa::pool_shared: {N} tokens do not split into {S} frames")
     P = N // S
-    nh = -(-int(grid) // int(kp)) if kp > 0 else 0
-    npool = nh * nh
+    npool = -(-int(grid_h) // int(kp)) * -(-int(grid_w) // int(kp))
     if not _rows_ok(k, 8):
         k = k.contiguous()
     if not _rows_ok(v, 8):
@@ -580,27 +585,27 @@ def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid: i
     pk = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
     pv = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
     size = torch.empty(B, H, S, npool, device=dev, dtype=torch.float32)
-    assign = (torch.empty(B, H, S, grid * grid, device=dev, dtype=torch.int32) if want_assign
-              else torch.empty(0, device=dev, dtype=torch.int32))
+    assign = (torch.empty(B, H, S, grid_h * grid_w, device=dev, dtype=torch.int32)
+              if want_assign else torch.empty(0, device=dev, dtype=torch.int32))
     if pk.numel() == 0:
         return pk, pv, size, assign
     with torch.cuda.device(dev):
         rc = lib().gpa_pool_shared_bf16(
             k.data_ptr(), v.data_ptr(), pk.data_ptr(), pv.data_ptr(), size.data_ptr(),
-            assign.data_ptr() if want_assign else None, B, H, S, P, pts, grid, kp, D,
+            assign.data_ptr() if want_assign else None, B, H, S, P, pts, grid_h, grid_w, kp, D,
             _st(k, 0), _st(k, 1), _rs(k, 2), _st(v, 0), _st(v, 1), _rs(v, 2), _stream(dev))
     _check(rc, "gpa::pool_shared")
     return pk, pv, size, assign
 
 
 @pool_shared.register_fake
-def _pool_shared_fake(k, v, frames, pts, grid, kp, want_assign):
+def _pool_shared_fake(k, v, frames, pts, grid_h, grid_w, kp, want_assign):
     B, H, N, D = k.shape
-    nh = -(-grid // kp)
-    npool = nh * nh
+    npool = -(-grid_h // kp) * -(-grid_w // kp)
     return (k.new_empty(B, H, frames * npool, D), k.new_empty(B, H, frames * npool, D),
             k.new_empty(B, H, frames, npool, dtype=torch.float32),
-            k.new_empty((B, H, frames, grid * grid) if want_assign else (0,), dtype=torch.int32))
+            k.new_empty((B, H, frames, grid_h * grid_w) if want_assign else (0,),
+                        dtype=torch.int32))
 
 
 # --------------------------------------------------------------------------

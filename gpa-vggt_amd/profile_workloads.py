@@ -117,7 +117,7 @@ def main(argv=None) -> int:
         kk = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
         vv = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
         for _ in range(reps):
-            torch.ops.gpa.pool_shared(kk, vv, 200, 5, 37, 8, False)
+            torch.ops.gpa.pool_shared(kk, vv, 200, 5, 37, 37, 8, False)
         torch.cuda.synchronize()
         print(f"pool 16x200 frames kp 8 x {reps} done", flush=True)
         del kk, vv

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 9
+#define GPA_ABI_VERSION 10
 
 enum {
   GPA_OK = 0,
@@ -279,28 +279,30 @@ int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H, int6
 /*
  * Pooled summaries of the frame-special shared K/V set.  For every
  * (b, h, frame s) and its patch keys x_p = k[b, h, s*P + pts + p, :]
- * (p < grid*grid, D = 64):
- *   seeds y_g: the patches (gy*kp, gx*kp) of the grid, g = gy*nh + gx,
- *              nh = ceil(grid/kp), npool = nh*nh (<= 64)
+ * (p < grid_h*grid_w on a grid_h-row, grid_w-column patch grid, row-major;
+ * D = 64):
+ *   seeds y_g: the patches (gy*kp, gx*kp), g = gy*nw + gx, nh = ceil(grid_h/kp),
+ *              nw = ceil(grid_w/kp), npool = nh*nw (<= 64)
  *   assign a_p = argmax_g bf16(bf16(x_p/max(|x_p|,1e-6)) . bf16(y_g/max(|y_g|,1e-6)))
  *              (fp32 dots rounded to bf16; the lowest g wins ties)
  *   size[b,h,s,g]         = #{p : a_p = g}                                (fp32)
  *   pooled_k[b,h,s*npool+g,:] = sum_{a_p=g} k_p / max(size, 1)           (bf16)
  *   pooled_v likewise from v (same token positions).
  * pooled_k / pooled_v are contiguous [B, H, S*npool, 64], size [B, H, S, npool];
- * assign (nullable) receives a_p as int32 [B, H, S, grid*grid].  k and v
- * rows 16-byte aligned, unit feature stride.  The sums run in fp32 in a
- * fixed order, so the means are deterministic (the reference's scatter_add_
- * sums with atomics in a run-dependent order).
- * Replaces `_pool` of vggt/layers/attention.py:113-140 (the einsum at :130
- * under bf16 autocast) and the pool sizes behind the bias of :142-146; the
- * reference module interface has no such entry point (it runs these as
- * torch ops).
+ * assign (nullable) receives a_p as int32 [B, H, S, grid_h*grid_w].  k and v
+ * rows 16-byte aligned, unit feature stride; grid_h*grid_w <= 4096.  More
+ * than 64 seeds: GPA_E_UNSUPPORTED.  The sums run in fp32 in a fixed order,
+ * so the means are deterministic (the reference's scatter_add_ sums with
+ * atomics in a run-dependent order).
+ * Replaces `_pool` of vggt/layers/attention.py:113-140 (ph = grid_h,
+ * pw = grid_w; the einsum at :130 under bf16 autocast) and the pool sizes
+ * behind the bias of :142-146; the reference module interface has no such
+ * entry point (it runs these as torch ops).
  */
 int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* pooled_v,
                          float* size, int32_t* assign, int64_t B, int64_t H, int64_t S,
-                         int64_t P, int64_t pts, int64_t grid, int64_t kp, int64_t D,
-                         int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                         int64_t P, int64_t pts, int64_t grid_h, int64_t grid_w, int64_t kp,
+                         int64_t D, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                          int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream);
 
 /*

@@ -59,21 +59,21 @@ def test_frame_positions_layout():
     assert pos[5 + 37].tolist() == [2, 1] and pos[-1].tolist() == [37, 37]
 
 
-def _pool_bruteforce(k5, v5, pts, grid, kp):
+def _pool_bruteforce(k5, v5, pts, grid_h, grid_w, kp):
     B, H, S, P, D = k5.shape
-    seeds_yx = [(y, x) for y in range(0, grid, kp) for x in range(0, grid, kp)]
+    seeds_yx = [(y, x) for y in range(0, grid_h, kp) for x in range(0, grid_w, kp)]
     npool = len(seeds_yx)
     pk = np.zeros((B, H, S, npool, D))
     pv = np.zeros((B, H, S, npool, D))
     size = np.zeros((B, H, S, npool))
-    assign = np.zeros((B, H, S, grid * grid), dtype=np.int64)
+    assign = np.zeros((B, H, S, grid_h * grid_w), dtype=np.int64)
     k = k5.double().numpy()
     v = v5.double().numpy()
     for b in range(B):
         for h in range(H):
             for s in range(S):
                 patches = k[b, h, s, pts:]
-                seeds = np.stack([patches[y * grid + x] for y, x in seeds_yx])
+                seeds = np.stack([patches[y * grid_w + x] for y, x in seeds_yx])
                 pn = patches / np.maximum(np.linalg.norm(patches, axis=1, keepdims=True), 1e-6)
                 sn = seeds / np.maximum(np.linalg.norm(seeds, axis=1, keepdims=True), 1e-6)
                 sc = pn @ sn.T
@@ -89,20 +89,23 @@ def _pool_bruteforce(k5, v5, pts, grid, kp):
     return pk, pv, size, assign
 
 
-def test_pool_shared_matches_bruteforce():
+@pytest.mark.parametrize("gh,gw,kp,npool", [(7, 7, 3, 9), (5, 8, 3, 6), (8, 5, 3, 6),
+                                            (4, 10, 4, 3)])
+def test_pool_shared_matches_bruteforce(gh, gw, kp, npool):
+    """Square and rectangular patch grids (ph != pw): the seeds walk the rows
+    of a row-major grid_h x grid_w layout."""
     g = torch.Generator().manual_seed(1)
-    B, H, S, pts, grid, kp, D = 1, 2, 3, 5, 7, 3, 16
-    k5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
-    v5 = torch.randn(B, H, S, pts + grid * grid, D, generator=g)
-    pk, pv, size, assign = A.pool_shared_torch(k5, v5, pts, grid, kp)
-    bpk, bpv, bsize, bassign = _pool_bruteforce(k5, v5, pts, grid, kp)
-    npool = 9
+    B, H, S, pts, D = 1, 2, 3, 5, 16
+    k5 = torch.randn(B, H, S, pts + gh * gw, D, generator=g)
+    v5 = torch.randn(B, H, S, pts + gh * gw, D, generator=g)
+    pk, pv, size, assign = A.pool_shared_torch(k5, v5, pts, gh, gw, kp)
+    bpk, bpv, bsize, bassign = _pool_bruteforce(k5, v5, pts, gh, gw, kp)
     assert np.array_equal(assign.numpy(), bassign)
     assert np.array_equal(size.numpy(), bsize)
     assert np.abs(pk.double().numpy().reshape(B, H, S, npool, D) - bpk).max() < 1e-5
     assert np.abs(pv.double().numpy().reshape(B, H, S, npool, D) - bpv).max() < 1e-5
     # every seed belongs to its own group: no empty summary
-    assert (size > 0).all() and (size.sum(-1) == grid * grid).all()
+    assert (size > 0).all() and (size.sum(-1) == gh * gw).all()
 
 
 def test_shifted_texture_images_are_translations():

@@ -153,7 +153,7 @@ def test_frame_special_block_attention_matches_reference(dev, kp):
         # the device's pool assignment, from the module's own K/V
         _, kd, vd = blk.attn.qk(xn, rope)
         if kp > 0:
-            _, _, size_d, assign_d = A.pool_shared_set(kd, vd, FRAMES, PTS, GRID, kp, True)
+            _, _, size_d, assign_d = A.pool_shared_set(kd, vd, FRAMES, PTS, GRID, GRID, kp, True)
     q, k, v = _qkv_ref(blk, xn, pos)
     q16, k16, v16 = q.bfloat16().float(), k.bfloat16().float(), v
     k5, v5 = k16.view(1, 16, FRAMES, P, 64), v16.view(1, 16, FRAMES, P, 64)
@@ -269,43 +269,54 @@ def test_qk_norm_rope_other_head_counts_and_strides(dev, B, H, pad):
         assert (err <= 1e-5 * want.abs() + 1e-5).all(), f"max err {err.max().item():.3e}"
 
 
-def _pool_bf16_fp64(x: torch.Tensor, grid: int, kp: int):
+def _pool_bf16_fp64(x: torch.Tensor, gh: int, gw: int, kp: int):
     """fp64 scores of bf16-rounded normalised rows against bf16-rounded
     normalised seeds (the einsum of attention.py:130 under bf16 autocast,
-    before its own bf16 rounding): x [G, grid*grid, 64] -> [G, grid*grid, npool]."""
+    before its own bf16 rounding): x [G, gh*gw, 64] -> [G, gh*gw, npool]."""
     def nb(t):
         t = t.float()
         return (t / t.norm(dim=-1, keepdim=True).clamp_min(1e-6)).bfloat16().double()
     G = x.shape[0]
-    seeds = x.view(G, grid, grid, 64)[:, ::kp, ::kp].reshape(G, -1, 64)
+    seeds = x.view(G, gh, gw, 64)[:, ::kp, ::kp].reshape(G, -1, 64)
     return torch.einsum("gpd,gsd->gps", nb(x), nb(seeds))
 
 
-@pytest.mark.parametrize("kp", [8, 5])
-def test_pool_shared_kernel_matches_reference(dev, kp):
+@pytest.mark.parametrize("gh,gw,kp", [
+    (37, 37, 8), (37, 37, 5),     # the 518 x 518 grid: 25 and 64 seeds
+    (28, 37, 8), (37, 28, 5),     # 392 x 518 and 518 x 392 images: 20 and 48 seeds
+    (13, 50, 7),                  # ragged last tile and lattice row
+    (64, 64, 8),                  # 4096 patches, 64 seeds: the kernel's limits
+    (1, 1, 8),                    # one patch, one seed
+])
+def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     """gpa::pool_shared against the scores in fp64 (assignment, except rows
     whose best two scores are within two bf16 steps, where the bf16 rounding
     of the reference's scores decides) and, given its own assignment, exact
     sizes and fp64 means of the K and V rows; bit-identical on a second call
-    and on strided V rows."""
-    g = torch.Generator(device=dev).manual_seed(kp)
+    and on strided V rows.  Square and rectangular patch grids."""
+    g = torch.Generator(device=dev).manual_seed(gh * 100 + gw + kp)
     B, H, S = 1, 4, 3
-    k = (torch.randn(B, H, S * P, 64, generator=g, device=dev) * 0.7).bfloat16()
-    v = torch.randn(B, H, S * P, 64, generator=g, device=dev).bfloat16()
-    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, GRID, kp, True)
-    nh = -(-GRID // kp)
-    npool = nh * nh
+    P_ = PTS + gh * gw
+    npatch = gh * gw
+    k = (torch.randn(B, H, S * P_, 64, generator=g, device=dev) * 0.7).bfloat16()
+    v = torch.randn(B, H, S * P_, 64, generator=g, device=dev).bfloat16()
+    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, True)
+    npool = -(-gh // kp) * -(-gw // kp)
     assert pk.shape == (B, H, S * npool, 64) and size.shape == (B, H, S, npool)
-    kp5 = k.view(B, H, S, P, 64)[:, :, :, PTS:].reshape(-1, GRID * GRID, 64).cpu()
-    vp5 = v.view(B, H, S, P, 64)[:, :, :, PTS:].reshape(-1, GRID * GRID, 64).cpu()
-    sc = _pool_bf16_fp64(kp5, GRID, kp)
-    top2 = sc.topk(2, dim=-1).values
-    sure = (top2[..., 0] - top2[..., 1]) > 2 * 2.0 ** -8
-    a = assign.cpu().long().reshape(-1, GRID * GRID)
+    assert assign.shape == (B, H, S, npatch)
+    kp5 = k.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+    vp5 = v.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+    sc = _pool_bf16_fp64(kp5, gh, gw, kp)
+    a = assign.cpu().long().reshape(-1, npatch)
+    if npool > 1:
+        top2 = sc.topk(2, dim=-1).values
+        sure = (top2[..., 0] - top2[..., 1]) > 2 * 2.0 ** -8
+        assert sure.float().mean() > 0.5
+    else:
+        sure = torch.ones_like(a, dtype=torch.bool)
     assert torch.equal(a[sure], sc.argmax(-1)[sure])
-    assert sure.float().mean() > 0.5
     # seeds belong to their own group
-    seeds_pos = [(y * GRID + x) for y in range(0, GRID, kp) for x in range(0, GRID, kp)]
+    seeds_pos = [(y * gw + x) for y in range(0, gh, kp) for x in range(0, gw, kp)]
     assert torch.equal(a[:, seeds_pos], torch.arange(npool).expand(a.shape[0], npool))
     onehot = torch.nn.functional.one_hot(a, npool).double()          # [G, p, npool]
     cnt = onehot.sum(1)
@@ -317,13 +328,13 @@ def test_pool_shared_kernel_matches_reference(dev, kp):
         err = (got - want).abs()
         assert (err <= 2.0 ** -8 * want.abs() + 1e-6).all(), f"max err {err.max().item():.3e}"
     # the torch restatement on the same device agrees on the sure rows
-    _, _, _, a_t = A.pool_shared_torch(k.view(B, H, S, P, 64), v.view(B, H, S, P, 64),
-                                       PTS, GRID, kp)
-    assert torch.equal(a_t.cpu().reshape(-1, GRID * GRID)[sure], a[sure])
+    _, _, _, a_t = A.pool_shared_torch(k.view(B, H, S, P_, 64), v.view(B, H, S, P_, 64),
+                                       PTS, gh, gw, kp)
+    assert torch.equal(a_t.cpu().reshape(-1, npatch)[sure], a[sure])
     # deterministic sums (fixed order), and strided rows give the same result
-    pk2, pv2, size2, _ = torch.ops.gpa.pool_shared(k, v, S, PTS, GRID, kp, False)
+    pk2, pv2, size2, _ = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, False)
     assert torch.equal(pk2, pk) and torch.equal(pv2, pv) and torch.equal(size2, size)
-    wide = torch.zeros(B, H, S * P, 128, device=dev, dtype=torch.bfloat16)
+    wide = torch.zeros(B, H, S * P_, 128, device=dev, dtype=torch.bfloat16)
     wide[..., 32:96] = v
-    pk3, pv3, _, _ = torch.ops.gpa.pool_shared(k, wide[..., 32:96], S, PTS, GRID, kp, False)
+    pk3, pv3, _, _ = torch.ops.gpa.pool_shared(k, wide[..., 32:96], S, PTS, gh, gw, kp, False)
     assert torch.equal(pk3, pk) and torch.equal(pv3, pv)

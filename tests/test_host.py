@@ -210,7 +210,7 @@ def test_qk_norm_rope_empty_is_a_no_op():
 
 def _pool(**kw):
     args = dict(k=FAKE, v=FAKE, pk=FAKE, pv=FAKE, size=FAKE, assign=None, B=1, H=2, S=3, P=1374,
-                pts=5, grid=37, kp=8, D=64, ksb=0, ksh=263808, ksn=64, vsb=0, vsh=263808, vsn=64,
+                pts=5, gh=37, gw=37, kp=8, D=64, ksb=0, ksh=263808, ksn=64, vsb=0, vsh=263808, vsn=64,
                 stream=None)
     args.update(kw)
     return _native.lib().gpa_pool_shared_bf16(*args.values())
@@ -224,6 +224,10 @@ def _pool(**kw):
     (dict(size=None), _native.GPA_E_INVALID),
     (dict(P=1000), _native.GPA_E_INVALID),                  # frame too short for the grid
     (dict(kp=4), _native.GPA_E_UNSUPPORTED),                # 100 seeds > 64
+    (dict(gh=28, kp=4), _native.GPA_E_UNSUPPORTED),         # 7 x 10 = 70 seeds > 64
+    (dict(gh=65, gw=64, P=4165, kp=9), _native.GPA_E_UNSUPPORTED),  # 4160 patches > 4096
+    (dict(gh=-1), _native.GPA_E_INVALID),
+    (dict(gw=38), _native.GPA_E_INVALID),                   # 37 x 38 patches + 5 > P
     (dict(ksn=60), _native.GPA_E_INVALID),                  # misaligned k rows
     (dict(vsn=63), _native.GPA_E_INVALID),                  # misaligned v rows
     (dict(vsn=68), _native.GPA_E_INVALID),                  # v rows not 16-byte aligned
@@ -236,6 +240,7 @@ def test_pool_shared_argument_errors(kw, code):
 def test_pool_shared_empty_is_a_no_op():
     assert _pool(B=0) == _native.GPA_OK
     assert _pool(S=0) == _native.GPA_OK
+    assert _pool(gh=0) == _native.GPA_OK
 
 
 def _metric(**kw):
