@@ -85,10 +85,24 @@ class GpaConfig:
     fused_norms: bool = True           # residual + LayerScale + LayerNorm kernel (bf16 blocks)
     vit_depth: int = 24                # DINOv2 ViT-L/14 blocks
     dpt_blocks: Tuple[int, ...] = (4, 11, 17, 23)   # outputs kept (aggregator.py:296)
+    img_width: Optional[int] = None    # image width; None: square (img_size x img_size)
+
+    @property
+    def grid_h(self) -> int:
+        """Patch rows (ph, `patch_height` of attention.py:42)."""
+        return self.img_size // self.patch_size
+
+    @property
+    def grid_w(self) -> int:
+        """Patch columns (pw, `patch_width` of attention.py:41)."""
+        return (self.img_width or self.img_size) // self.patch_size
 
     @property
     def grid(self) -> int:
-        return self.img_size // self.patch_size
+        """Side of a square patch grid."""
+        if self.grid_h != self.grid_w:
+            raise ValueError(f"{self.grid_h} x {self.grid_w} patch grid is not square")
+        return self.grid_h
 
     @property
     def num_special(self) -> int:
@@ -96,7 +110,7 @@ class GpaConfig:
 
     @property
     def tokens_per_frame(self) -> int:
-        return self.grid * self.grid + self.num_special
+        return self.grid_h * self.grid_w + self.num_special
 
     def global_merging(self, block: int) -> Optional[int]:
         """The block index if global block `block` merges K/V (aggregator.py:317-325)."""
@@ -251,8 +265,8 @@ class GpaAttention(nn.Module):
             gen = torch.Generator(device=x.device)
             gen.manual_seed(MERGE_GENERATOR_SEED)
             r = int(N * self.merge_ratio)
-            g = self.cfg.grid
-            m = token_merge_bipartite2d(x, g, g, self.cfg.merge_grid, self.cfg.merge_grid, r,
+            m = token_merge_bipartite2d(x, self.cfg.grid_w, self.cfg.grid_h, self.cfg.merge_grid,
+                                        self.cfg.merge_grid, r,
                                         False, gen, metric_dim=self.cfg.merge_metric_dim,
                                         num_special=self.cfg.num_special)
             k = m.heads(k, "mean")
@@ -281,8 +295,8 @@ class GpaAttention(nn.Module):
                 else torch.bfloat16
             q, k, v = q.to(dt), k.to(dt), v.to(dt)
         H, D = self.heads, self.head_dim
-        pts, g = self.cfg.num_special, self.cfg.grid
-        P = g * g + pts
+        pts, gh, gw = self.cfg.num_special, self.cfg.grid_h, self.cfg.grid_w
+        P = gh * gw + pts
         S = N // P
         if S * P != N:
             raise ValueError(f"frame_special: {N} tokens is not a multiple of {P}")
@@ -301,7 +315,7 @@ class GpaAttention(nn.Module):
         out_a, lse_a = attention_keybias(q_f, own_k, own_v, None, self.scale, return_lse=True)
         del own_k, own_v
         if kp > 0:
-            pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, g, g, kp)
+            pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, gh, gw, kp)
             if self.merge_log is not None:
                 self.merge_log.append({"kind": "pool", "frames": S, "pool_size": pool_size})
             sh_k = torch.cat([k5[:, :, :, :pts].reshape(B, H, S * pts, D), pooled_k], dim=2)
@@ -425,7 +439,7 @@ class DinoV2Reg(nn.Module):
         dim = cfg.embed_dim
         self.patch = nn.Conv2d(3, dim, cfg.patch_size, cfg.patch_size)
         self.cls_token = nn.Parameter(torch.zeros(1, 1, dim))
-        self.pos_embed = nn.Parameter(torch.zeros(1, cfg.grid * cfg.grid + 1, dim))
+        self.pos_embed = nn.Parameter(torch.zeros(1, cfg.grid_h * cfg.grid_w + 1, dim))
         self.register_tokens = nn.Parameter(torch.zeros(1, cfg.num_register_tokens, dim))
         self.blocks = nn.ModuleList(
             Block(dim, cfg.num_heads, cfg.mlp_ratio, 1.0, False, 1e-6, cfg)
@@ -516,7 +530,8 @@ class GpaAggregator(nn.Module):
             self.tracer.mark(name)
 
     def positions(self, device) -> torch.Tensor:
-        return frame_positions(self.cfg.grid, self.cfg.num_special, device)
+        return frame_positions(self.cfg.grid_h, self.cfg.num_special, device,
+                               grid_w=self.cfg.grid_w)
 
     def embed(self, images: torch.Tensor) -> torch.Tensor:
         """[B, S, 3, H, W] in [0, 1] -> tokens [B*S, P, C] in the model dtype."""
@@ -550,10 +565,13 @@ class GpaAggregator(nn.Module):
         return outputs
 
 
-def frame_positions(grid: int, num_special: int, device="cpu") -> torch.Tensor:
-    """[P, 2] RoPE positions of one frame: specials at (0, 0), patch (y, x)
-    at (y + 1, x + 1), row-major (aggregator.py:279-288, rope.py:54-65)."""
-    yx = torch.cartesian_prod(torch.arange(grid, device=device), torch.arange(grid, device=device))
+def frame_positions(grid: int, num_special: int, device="cpu",
+                    grid_w: Optional[int] = None) -> torch.Tensor:
+    """[P, 2] RoPE positions of one frame on a grid x grid_w patch grid
+    (grid_w None: square): specials at (0, 0), patch (y, x) at (y + 1, x + 1),
+    row-major (aggregator.py:279-288, rope.py:54-65)."""
+    gw = grid if grid_w is None else grid_w
+    yx = torch.cartesian_prod(torch.arange(grid, device=device), torch.arange(gw, device=device))
     return torch.cat((torch.zeros(num_special, 2, dtype=yx.dtype, device=device), yx + 1))
 
 
@@ -597,16 +615,17 @@ def build_aggregator(cfg: Optional[GpaConfig] = None, device="cuda", dtype=torch
     return model.to(dtype).eval()
 
 
-def shifted_texture_images(frames: int, size: int = 518, shift: int = 64, seed: int = 0,
+def shifted_texture_images(frames: int, size=518, shift: int = 64, seed: int = 0,
                            device="cpu", dtype=torch.float32) -> torch.Tensor:
-    """[1, frames, 3, size, size] i.i.d. U[0,1] RGB crops of one shared random
-    texture at per-frame random offsets in [0, shift)^2: every frame is a
-    translated view of the same content."""
+    """[1, frames, 3, h, w] (size = h = w, or size = (h, w)) i.i.d. U[0,1]
+    RGB crops of one shared random texture at per-frame random offsets in
+    [0, shift)^2: every frame is a translated view of the same content."""
+    h, w = (size, size) if isinstance(size, int) else size
     g = torch.Generator(device=device)
     g.manual_seed(seed)
-    tex = torch.rand(3, size + shift, size + shift, generator=g, device=device)
+    tex = torch.rand(3, h + shift, w + shift, generator=g, device=device)
     off = torch.randint(0, shift, (frames, 2), generator=g, device=device).tolist()
-    imgs = torch.stack([tex[:, y:y + size, x:x + size] for y, x in off])
+    imgs = torch.stack([tex[:, y:y + h, x:x + w] for y, x in off])
     return imgs.unsqueeze(0).to(dtype)
 
 
@@ -642,19 +661,23 @@ def aggregator_flops(cfg: GpaConfig, frames: int) -> Dict[str, float]:
     dense_block = 2.0 * T * (3 * C * C + C * C + 2 * C * hid)
     frame_attn = 4.0 * frames * cfg.num_heads * P * P * Hd
     out = {"dense": dense_block * (cfg.vit_depth + 2 * cfg.depth)
-           + 2.0 * frames * cfg.grid ** 2 * 3 * cfg.patch_size ** 2 * C,
+           + 2.0 * frames * cfg.grid_h * cfg.grid_w * 3 * cfg.patch_size ** 2 * C,
            "frame_attn": frame_attn * (cfg.vit_depth + cfg.depth),
            "global_attn": 0.0, "similarity": 0.0}
-    pts, g = cfg.num_special, cfg.grid
+    pts, gh, gw = cfg.num_special, cfg.grid_h, cfg.grid_w
     from merging.merge import num_dst_tokens
     for i in range(cfg.depth):
         kind = cfg.block_kind(i)
         if kind == "frame_special":
-            npool = (-(-g // cfg.broadcast_pool)) ** 2 if cfg.broadcast_pool > 0 else 0
+            kp = cfg.broadcast_pool
+            if kp < 0:      # plain attention over each frame's own tokens
+                out["global_attn"] += 4.0 * frames * cfg.num_heads * P * P * Hd
+                continue
+            npool = (-(-gh // kp)) * (-(-gw // kp)) if kp > 0 else 0
             out["global_attn"] += 4.0 * frames * cfg.num_heads * P * (P - pts) * Hd
             out["global_attn"] += 4.0 * cfg.num_heads * T * frames * (pts + npool) * Hd
         elif kind == "merged":
-            nd = num_dst_tokens(frames, g, g, cfg.merge_grid, cfg.merge_grid, pts, False)
+            nd = num_dst_tokens(frames, gw, gh, cfg.merge_grid, cfg.merge_grid, pts, False)
             ns = T - nd
             r = min(ns, int(T * cfg.block_merge_ratio(i)))
             out["global_attn"] += 4.0 * cfg.num_heads * T * (T - r) * Hd

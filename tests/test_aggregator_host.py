@@ -108,6 +108,30 @@ def test_pool_shared_matches_bruteforce(gh, gw, kp, npool):
     assert (size > 0).all() and (size.sum(-1) == gh * gw).all()
 
 
+def test_frame_positions_rectangular():
+    pos = A.frame_positions(3, 5, grid_w=4)
+    assert pos.shape == (17, 2)
+    assert (pos[:5] == 0).all()
+    want = [[y + 1, x + 1] for y in range(3) for x in range(4)]
+    assert pos[5:].tolist() == want
+
+
+def test_rectangular_config_and_embed():
+    """A 42 x 56 image: 3 patch rows x 4 columns (ph x pw), row-major."""
+    cfg = A.GpaConfig(vit_depth=0, depth=1, img_size=42, img_width=56)
+    assert (cfg.grid_h, cfg.grid_w, cfg.tokens_per_frame) == (3, 4, 17)
+    with pytest.raises(ValueError):
+        cfg.grid
+    model = A.GpaAggregator(cfg)
+    A.init_random_(model)
+    imgs = A.shifted_texture_images(3, size=(42, 56), shift=4)
+    assert imgs.shape == (1, 3, 3, 42, 56)
+    with torch.no_grad():
+        tok = model.embed(imgs)
+    assert tok.shape == (3, 17, 1024)
+    assert model.positions("cpu").shape == (17, 2)
+
+
 def test_shifted_texture_images_are_translations():
     imgs = A.shifted_texture_images(4, size=40, shift=6, seed=3)
     assert imgs.shape == (1, 4, 3, 40, 40)
@@ -157,3 +181,22 @@ def test_aggregator_flops_closed_form():
     assert f["global_attn"] == pytest.approx(9 * (own + shared) + merged, rel=1e-12)
     assert f["similarity"] == pytest.approx(15 * 2.0 * 207_955 * 66_845 * 128, rel=1e-12)
     assert f["frame_attn"] == pytest.approx(48 * 4.0 * 200 * H * 1374 * 1374 * D, rel=1e-12)
+
+
+def test_aggregator_flops_rectangular_and_frame_only():
+    """392 x 518 images (28 x 37 patches): 20 pooled summaries per frame at
+    kp 8; kp < 0 is plain attention over each frame's own tokens."""
+    cfg = A.GpaConfig(img_size=392, img_width=518)
+    P = 28 * 37 + 5
+    T, H, D = 200 * P, 16, 64
+    f = A.aggregator_flops(cfg, 200)
+    own = 4.0 * 200 * H * P * (P - 5) * D
+    shared = 4.0 * H * T * 200 * (5 + 20) * D
+    f_nomerge = A.aggregator_flops(A.GpaConfig(img_size=392, img_width=518, merging=None), 200)
+    plain = 4.0 * H * T * T * D
+    assert f_nomerge["global_attn"] == pytest.approx(9 * (own + shared) + 15 * plain, rel=1e-12)
+    assert f["frame_attn"] == pytest.approx(48 * 4.0 * 200 * H * P * P * D, rel=1e-12)
+    f_neg = A.aggregator_flops(A.GpaConfig(img_size=392, img_width=518, merging=None,
+                                           broadcast_pool=-1), 200)
+    assert f_neg["global_attn"] == pytest.approx(9 * 4.0 * 200 * H * P * P * D + 15 * plain,
+                                                 rel=1e-12)

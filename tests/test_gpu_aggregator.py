@@ -46,8 +46,8 @@ def _rope_ref(x: torch.Tensor, pos: torch.Tensor, freq: float = 100.0) -> torch.
     return out.float()
 
 
-def _block(dev, seed=0):
-    cfg = A.GpaConfig()
+def _block(dev, seed=0, gh=GRID, gw=GRID):
+    cfg = A.GpaConfig(img_size=14 * gh, img_width=14 * gw)
     blk = A.Block(1024, 16, 4.0, 1.0, True, 1e-5, cfg).to(dev)
     A.init_random_(blk, seed)
     with torch.no_grad():   # non-trivial qk-norm affine parameters
@@ -58,9 +58,13 @@ def _block(dev, seed=0):
     return cfg, blk.bfloat16().eval()
 
 
-def _inputs(dev):
+def _inputs(dev, gh=GRID, gw=GRID):
+    """Tokens of FRAMES frames on a gh x gw patch grid (the first
+    gh*gw + PTS tokens of each 1,374-token frame of the shifted basis)."""
     x = W.shifted_basis_tokens(FRAMES, seed=4, device=dev).to(torch.bfloat16)
-    pos1 = A.frame_positions(GRID, PTS, dev)
+    p_ = gh * gw + PTS
+    x = x.view(1, FRAMES, P, -1)[:, :, :p_].reshape(1, FRAMES * p_, -1)
+    pos1 = A.frame_positions(gh, PTS, dev, grid_w=gw)
     return x, pos1.repeat(FRAMES, 1), A.Rope2D(100.0).table(pos1, 64)
 
 
@@ -112,16 +116,19 @@ def _compare(got: torch.Tensor, ref: torch.Tensor, what: str):
     assert rel_mean < 0.006, f"{what}: mean error {rel_mean:.3e} of mean |ref|"
 
 
-def test_merged_block_attention_matches_reference(dev):
-    cfg, blk = _block(dev)
-    x, pos, rope = _inputs(dev)
+@pytest.mark.parametrize("gh,gw", [(37, 37), (28, 37)])
+def test_merged_block_attention_matches_reference(dev, gh, gw):
+    """Square (518 x 518) and rectangular (392 x 518 images: 28 patch rows
+    x 37 columns, the reference module's default) patch grids."""
+    cfg, blk = _block(dev, gh=gh, gw=gw)
+    x, pos, rope = _inputs(dev, gh, gw)
     N = x.shape[1]
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
         xn = blk.norm1(x)
         got = blk.attn(xn, rope, 9)
         gen = torch.Generator(device=dev)
         gen.manual_seed(A.MERGE_GENERATOR_SEED)
-        m = token_merge_bipartite2d(xn, GRID, GRID, 2, 2, int(N * 0.98), False, gen,
+        m = token_merge_bipartite2d(xn, gw, gh, 2, 2, int(N * 0.98), False, gen,
                                     metric_dim=128, num_special=PTS)
     assert xn.dtype == torch.float32
     q, k, v = _qkv_ref(blk, xn, pos)
@@ -133,19 +140,22 @@ def test_merged_block_attention_matches_reference(dev):
     bias = size.log().view(1, 1, 1, -1)
     o, _ = attention_reference(*kernel_inputs(q, km, vm.float(), bias.expand(1, 16, 1, -1)),
                                blk.attn.scale)
-    _compare(got, _proj_ref(blk, o), "merged block")
+    _compare(got, _proj_ref(blk, o), f"merged block ({gh} x {gw})")
 
 
-@pytest.mark.parametrize("kp", [8, 5, 4, 0, -1])
-def test_frame_special_block_attention_matches_reference(dev, kp):
+@pytest.mark.parametrize("kp,gh,gw", [(8, 37, 37), (5, 37, 37), (4, 37, 37), (0, 37, 37),
+                                      (-1, 37, 37), (8, 28, 37), (4, 28, 37), (5, 37, 28)])
+def test_frame_special_block_attention_matches_reference(dev, kp, gh, gw):
     """The frame-special block for the pool strides the reference accepts
     (attention.py:106-108, 178-190): kp > 0 pooled summaries (the kernel up
-    to 64 seeds, kp 8 and 5; the torch restatement above, kp 4), kp = 0 the
-    special tokens only, kp < 0 plain frame attention."""
-    cfg, blk = _block(dev, seed=1)
+    to 64 seeds, e.g. kp 8 and 5 at 37 x 37; the torch restatement above,
+    kp 4), kp = 0 the special tokens only, kp < 0 plain frame attention; on
+    square and rectangular patch grids (ph x pw = gh x gw)."""
+    cfg, blk = _block(dev, seed=1, gh=gh, gw=gw)
     cfg.broadcast_pool = kp
     blk.attn.frame_special = True
-    x, pos, rope = _inputs(dev)
+    x, pos, rope = _inputs(dev, gh, gw)
+    P = gh * gw + PTS
     N = x.shape[1]
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
         xn = blk.norm1(x)
@@ -153,7 +163,7 @@ def test_frame_special_block_attention_matches_reference(dev, kp):
         # the device's pool assignment, from the module's own K/V
         _, kd, vd = blk.attn.qk(xn, rope)
         if kp > 0:
-            _, _, size_d, assign_d = A.pool_shared_set(kd, vd, FRAMES, PTS, GRID, GRID, kp, True)
+            _, _, size_d, assign_d = A.pool_shared_set(kd, vd, FRAMES, PTS, gh, gw, kp, True)
     q, k, v = _qkv_ref(blk, xn, pos)
     q16, k16, v16 = q.bfloat16().float(), k.bfloat16().float(), v
     k5, v5 = k16.view(1, 16, FRAMES, P, 64), v16.view(1, 16, FRAMES, P, 64)
@@ -163,15 +173,15 @@ def test_frame_special_block_attention_matches_reference(dev, kp):
             o, _ = attention_reference(*kernel_inputs(q16[:, :, s * P:(s + 1) * P], k5[:, :, s],
                                                       v5[:, :, s], None), blk.attn.scale)
             out[:, :, s * P:(s + 1) * P] = o
-        _compare(got, _proj_ref(blk, out), f"frame attention (kp {kp})")
+        _compare(got, _proj_ref(blk, out), f"frame attention (kp {kp}, {gh} x {gw})")
         return
     sp_k = k5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
     sp_v = v5[:, :, :, :PTS].reshape(1, 16, FRAMES * PTS, 64)
     extra_k, extra_v, extra_b = [sp_k], [sp_v], [torch.zeros(1, 16, 1, FRAMES * PTS)]
     if kp > 0:
         assign = assign_d.cpu().long()
-        npool = (-(-GRID // kp)) ** 2
-        onehot = F.one_hot(assign, npool).double()                     # [1,16,S,1369,np]
+        npool = (-(-gh // kp)) * (-(-gw // kp))
+        onehot = F.one_hot(assign, npool).double()                     # [1,16,S,gh*gw,np]
         cnt = onehot.sum(3)                                            # [1,16,S,np]
         assert torch.equal(cnt.float(), size_d.cpu())
         pk = torch.einsum("bhspg,bhspd->bhsgd", onehot, k5[:, :, :, PTS:].double()) / cnt[..., None]
@@ -182,19 +192,22 @@ def test_frame_special_block_attention_matches_reference(dev, kp):
     for s in range(FRAMES):
         kk = torch.cat([k5[:, :, s, PTS:]] + extra_k, dim=2)
         vv = torch.cat([v5[:, :, s, PTS:]] + extra_v, dim=2)
-        bias = torch.cat([torch.zeros(1, 16, 1, GRID * GRID)] + extra_b, dim=3)
+        bias = torch.cat([torch.zeros(1, 16, 1, gh * gw)] + extra_b, dim=3)
         o, _ = attention_reference(*kernel_inputs(q16[:, :, s * P:(s + 1) * P], kk, vv, bias),
                                    blk.attn.scale)
         out[:, :, s * P:(s + 1) * P] = o
-    _compare(got, _proj_ref(blk, out), f"frame-special block (kp {kp})")
+    _compare(got, _proj_ref(blk, out), f"frame-special block (kp {kp}, {gh} x {gw})")
 
 
-def test_small_aggregator_runs_every_global_path(dev):
+@pytest.mark.parametrize("hw", [(518, 518), (392, 518)])
+def test_small_aggregator_runs_every_global_path(dev, hw):
     cfg = A.GpaConfig(depth=3, vit_depth=1, early_frame_split=1, merging=1,
-                      core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2))
+                      core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2),
+                      img_size=hw[0], img_width=hw[1])
     assert [cfg.block_kind(i) for i in range(3)] == ["frame_special", "merged", "merged"]
+    P = cfg.tokens_per_frame
     model = A.build_aggregator(cfg, device=dev, seed=2)
-    imgs = A.shifted_texture_images(FRAMES, device=dev).to(torch.bfloat16)
+    imgs = A.shifted_texture_images(FRAMES, size=hw, device=dev).to(torch.bfloat16)
     tracer = A.StageTimer()
     model.set_tracer(tracer)
     tracer.start()
