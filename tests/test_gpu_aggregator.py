@@ -351,3 +351,26 @@ def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     wide[..., 32:96] = v
     pk3, pv3, _, _ = torch.ops.gpa.pool_shared(k, wide[..., 32:96], S, PTS, gh, gw, kp, False)
     assert torch.equal(pk3, pk) and torch.equal(pv3, pv)
+
+
+def test_pool_shared_batches_and_strided_k(dev):
+    """B = 2 with batch strides of a head-major view (k and v sliced out of a
+    [B, 2H, N, 64] buffer, heads 1, 3, 5, 7): each (batch, head, frame) equals
+    the same group pooled on its own as a contiguous B = 1 tensor."""
+    g = torch.Generator(device=dev).manual_seed(77)
+    B, H, S, gh, gw, kp = 2, 4, 3, 28, 37, 8
+    P_ = PTS + gh * gw
+    big_k = (torch.randn(B, 2 * H, S * P_, 64, generator=g, device=dev) * 0.7).bfloat16()
+    big_v = torch.randn(B, 2 * H, S * P_, 64, generator=g, device=dev).bfloat16()
+    k, v = big_k[:, 1::2], big_v[:, 1::2]
+    assert not k.is_contiguous()
+    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, True)
+    for b in range(B):
+        for h in range(H):
+            kk = k[b:b + 1, h:h + 1].contiguous()
+            vv = v[b:b + 1, h:h + 1].contiguous()
+            pk1, pv1, size1, a1 = torch.ops.gpa.pool_shared(kk, vv, S, PTS, gh, gw, kp, True)
+            assert torch.equal(pk[b:b + 1, h:h + 1], pk1)
+            assert torch.equal(pv[b:b + 1, h:h + 1], pv1)
+            assert torch.equal(size[b:b + 1, h:h + 1], size1)
+            assert torch.equal(assign[b:b + 1, h:h + 1], a1)
