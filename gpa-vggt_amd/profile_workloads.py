@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|sharp|own|merge|front|pool|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|sharp|own|shared|merge|front|pool|qk|combine|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
@@ -12,9 +12,15 @@
          to the lazily moved softmax offset (not in `all`)
   own    own-frame attention of the frame-special split, 3,200 (frame, head)
          pairs x 1,374 queries x 1,369 keys, no bias, with LSE (not in `all`)
+  shared shared-set attention of the frame-special split, 16 heads x 274,800
+         queries x 6,000 keys (1,000 specials + 5,000 pooled), log-size bias,
+         with LSE (not in `all`)
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
   front  merge front end: 274,800 fp32 metric rows of 1024 -> bf16 [dst | src] x 128
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
+  qk     qk LayerNorm + 2D RoPE of a 200-frame block: the bf16 QKV projection
+         [1, 274800, 3072] to bf16 q and k, then to bf16 q and fp32 k
+  combine LSE combine of the frame-special split at 200 frames (bf16)
   sim16  the similarity workload in fp16
   attn16 the attention workload in fp16
   attn0  the attention workload with all-zero q, k, v (same shapes, bias and
@@ -45,8 +51,8 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "sim200", "sim1024", "attn", "sharp", "own", "merge", "front", "pool",
-                     "sim16", "attn16", "attn0", "copy", "all"):
+    if which not in ("sim", "sim200", "sim1024", "attn", "sharp", "own", "shared", "merge", "front",
+                     "pool", "qk", "combine", "sim16", "attn16", "attn0", "copy", "all"):
         print(__doc__, file=sys.stderr)
         return 2
 
@@ -121,6 +127,40 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"pool 16x200 frames kp 8 x {reps} done", flush=True)
         del kk, vv
+    if which in ("qk", "all"):
+        import gpa_aggregator as A
+        qkv = torch.randn(1, 200 * 1374, 3 * 1024, device=dev).bfloat16()
+        ln_w, ln_b = torch.ones(2, 64, device=dev), torch.zeros(2, 64, device=dev)
+        rope = A.Rope2D(100.0).table(A.frame_positions(37, 5, dev), 64)
+        for k_f32 in (False, True):
+            for _ in range(reps):
+                torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, rope.pos, rope.cs, 16, False,
+                                           k_f32)
+        torch.cuda.synchronize()
+        print(f"qk 274800 tokens x 16 heads (bf16 k, fp32 k) x {reps} done", flush=True)
+        del qkv
+    if which in ("combine", "all"):
+        oa = (torch.randn(200, 16, 1374, 64, device=dev) / 8).bfloat16()
+        la = torch.randn(200, 16, 1374, device=dev)
+        ob = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        lb = torch.randn(1, 16, 200 * 1374, device=dev)
+        for _ in range(reps):
+            torch.ops.gpa.lse_combine(oa, la, ob, lb, 200)
+        torch.cuda.synchronize()
+        print(f"combine 200 frames x 16 heads x 1374 x {reps} done", flush=True)
+        del oa, la, ob, lb
+    if which == "shared":
+        q = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        k = (torch.randn(1, 16, 6000, 64, device=dev) / 8).bfloat16()
+        v = (torch.randn(1, 16, 6000, 64, device=dev) / 8).bfloat16()
+        bias = torch.zeros(1, 16, 1, 6000, device=dev)
+        bias[..., 1000:] = torch.randint(1, 100, (1, 16, 1, 5000), device=dev).float().log()
+        bias = bias.bfloat16()
+        for _ in range(reps):
+            attention_keybias(q, k, v, bias, 0.125, return_lse=True)
+        torch.cuda.synchronize()
+        print(f"shared 16x274800x6000x64 x {reps} done", flush=True)
+        del q, k, v, bias
     if which in ("sim16", "all"):
         s, d = W.sim_inputs(device=dev)
         s, d = s.half(), d.half()

@@ -149,9 +149,10 @@ int gpa_attn_keybias_bf16(const void* q, const void* k, const void* v,
 
 /* The same on fp16 q, k, v and o (fp16 MFMA; P rounded to fp16 for P.V,
  * fp32 softmax and accumulation; same arguments and workspace).  The fixed
- * offset of the main pass sits 15 below the score bound, so P <= 2^15 fits
- * fp16, and is certified only where every row max is within 16 of the
- * bound (else the repair pass rescales lazily at 2^15).  Replaces
+ * offset sits 15 below the score bound, so P <= 2^15 fits fp16, and is
+ * certified only where every row max is within 16 of the bound; a wave that
+ * cannot certify it continues with an offset that moves lazily, whenever a
+ * tile's row max rises above the offset + 15.  Replaces
  * fused_attention.py:130-180 under fp16 autocast (its :139-144 cast). */
 int gpa_attn_keybias_f16(const void* q, const void* k, const void* v,
                          const void* bias, int bias_kind,

@@ -5,8 +5,8 @@
 workspace, so on the same inputs its outputs must be bit-identical.  Two
 calls in a row (the second on a smaller problem, so stale scratch contents
 from the first call are present) with a bias, the LSE and sharp logits that
-send some waves through the repair pass (whose flags live in the scratch);
-both calls go through the C ABI directly.
+send some waves onto the lazily moved offset (whose flags live in the
+scratch); both calls go through the C ABI directly.
 """
 import ctypes
 
