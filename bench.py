@@ -67,8 +67,11 @@ def e2e_latency(dev) -> dict:
       global blocks on the GPA schedule) on 200 frames of 518 x 518 images,
       with the reference defaults, and with the variant of 64 pooled patch
       summaries per frame in the shared set (pool stride 5) and every merged
-      block at 25 % keep (no core blocks).
-    Timing follows eval/bench_e2e.py: 2 warm-up calls, mean of 3.
+      block at 25 % keep (no core blocks);
+    * the same aggregator without GPA (vanilla VGGT) and, with the reference
+      defaults, as the fp16 accuracy-evaluation stack.
+    Timing follows eval/bench_e2e.py: 2 warm-up calls, mean of 3 (1 and 2 for
+    the vanilla and fp16 forwards).
     """
     import torch
     import gpa_aggregator as A
@@ -137,7 +140,25 @@ def e2e_latency(dev) -> dict:
         "gpa_speedup": round(ms / gpa_ms, 3),
         "reference_speedup": "2.58x at 200 frames (README.md:21, reference hardware not stated)"}
     log(f"[bench] aggregator 200 frames (vanilla): {ms:.1f} ms, GPA speed-up {ms / gpa_ms:.2f}x")
-    del vm, imgs
+    del vm
+    torch.cuda.empty_cache()
+    # The accuracy-evaluation stack of the reference (eval_co3d.py:152, 226):
+    # the fp16 model under fp16 autocast, reference defaults.  The fused
+    # residual + LayerNorm kernel is bf16-only, so those steps run as torch
+    # ops here; every other kernel has its fp16 twin.
+    f16 = torch.float16
+    fm = A.build_aggregator(cfg, device=dev, dtype=f16)
+    imgs16 = imgs.to(f16)
+
+    def run16():
+        with torch.no_grad(), torch.autocast("cuda", dtype=f16):
+            return fm(imgs16)
+    ms, peak = A.timed(run16, warmup=1, iters=2)
+    res["aggregator_200f_fp16_eval_stack"] = {
+        "ms": round(ms, 1), "peak_gib": round(peak, 2), "protocol": "1 warm-up call, mean of 2",
+        "workload": "reference defaults, fp16 model under fp16 autocast (eval_co3d.py:152, 226)"}
+    log(f"[bench] aggregator 200 frames (fp16 evaluation stack): {ms:.1f} ms")
+    del fm, imgs16, imgs
     torch.cuda.empty_cache()
     return res
 

@@ -1,5 +1,5 @@
 // Residual + LayerScale + LayerNorm of a pre-LN transformer block, fused,
-// bf16 in and out, one wave per token row.
+// bf16 (or fp16) in and out, one wave per token row.
 //
 // For a row x (C features) and, optionally, a branch output y:
 //   h   = bf16( x + bf16(gamma * y) )                  (y given)   else h = x
@@ -14,7 +14,10 @@
 // passes over the [tokens, C] activations (mul, add, layer_norm, the
 // autocast cast); here one read of x and y, and one write of h and out.
 // Either output may be omitted: without y the kernel is the block's first
-// LayerNorm; without an output it is the residual step alone.
+// LayerNorm; without an output it is the residual step alone.  The fp16
+// instantiation is the same chain under fp16 autocast on an fp16 model (the
+// reference's accuracy-evaluation stack): every bf16 rounding above becomes
+// an fp16 rounding.
 //
 // Lane l of a row's wave owns features 8l + 512i .. +8 (i < C/512), so
 // every load and store of the wave covers 1 KB of the row contiguously; the
@@ -41,13 +44,14 @@ struct LnArgs {
   float eps;
 };
 
-// fp32 -> bf16 -> fp32 as a real rounding step.  Without the empty asm the
+// fp32 -> 16-bit -> fp32 as a real rounding step.  Without the empty asm the
 // compiler contracts `x + (float)(__bf16)(y * g)` into one FMA and skips the
 // rounding between the product and the sum that the reference performs.
-__device__ __forceinline__ float round_bf16(float v) {
-  uint32_t u = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v) << 16;
+template <bool F16>
+__device__ __forceinline__ float round16(float v) {
+  uint32_t u = __builtin_bit_cast(uint16_t, f32_to_half<F16>(v));
   asm volatile("" : "+v"(u));
-  return __uint_as_float(u);
+  return half_to_f32<F16>(__builtin_bit_cast(__bf16, (uint16_t)u));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -56,7 +60,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int NC>  // C = 512 * NC
+template <int NC, bool F16>  // C = 512 * NC
 __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnArgs a) {
   constexpr int C = 512 * NC;
   const int lane = threadIdx.x & 63;
@@ -69,7 +73,7 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnA
   for (int i = 0; i < NC; ++i) {
     const bf16x8 xv = xr[64 * i];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[i][e] = (float)xv[e];
+    for (int e = 0; e < 8; ++e) h[i][e] = half_to_f32<F16>(xv[e]);
   }
   if (a.y != nullptr) {
     const bf16x8* yr = reinterpret_cast<const bf16x8*>(a.y + row * a.y_sn) + lane;
@@ -79,8 +83,8 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnA
       const bf16x8 yv = yr[64 * i], gv = gr[64 * i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float t = round_bf16((float)yv[e] * (float)gv[e]);   // bf16(gamma * y)
-        h[i][e] = round_bf16(h[i][e] + t);                         // bf16(x + t)
+        const float t = round16<F16>(half_to_f32<F16>(yv[e]) * half_to_f32<F16>(gv[e]));
+        h[i][e] = round16<F16>(h[i][e] + t);                   // 16-bit(x + 16-bit(gamma * y))
       }
     }
     if (a.h_out != nullptr) {
@@ -89,7 +93,7 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnA
       for (int i = 0; i < NC; ++i) {
         bf16x8 hv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hv[e] = (__bf16)h[i][e];
+        for (int e = 0; e < 8; ++e) hv[e] = f32_to_half<F16>(h[i][e]);
         hr[64 * i] = hv;
       }
     }
@@ -120,7 +124,8 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnA
     bf16x8 ov;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      ov[e] = (__bf16)__builtin_fmaf((h[i][e] - mean) * rstd, (float)wv[e], (float)bv[e]);
+      ov[e] = f32_to_half<F16>(__builtin_fmaf((h[i][e] - mean) * rstd, half_to_f32<F16>(wv[e]),
+                                              half_to_f32<F16>(bv[e])));
     orow[64 * i] = ov;
   }
 }
@@ -130,30 +135,32 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void residual_layernorm_kernel(LnA
 
 using namespace gpa;
 
-extern "C" int gpa_residual_layernorm_bf16(const void* x, const void* y, const void* gamma,
-                                           const void* ln_weight, const void* ln_bias, float eps,
-                                           int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn,
-                                           void* h_out, int64_t h_sn, void* ln_out, int64_t ln_sn,
-                                           void* stream) {
+namespace {
+
+// Shared by the bf16 and fp16 entry points; `fn` names the entry point in
+// error messages.
+template <bool F16>
+int ln_run(const char* fn, const void* x, const void* y, const void* gamma, const void* ln_weight,
+           const void* ln_bias, float eps, int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn,
+           void* h_out, int64_t h_sn, void* ln_out, int64_t ln_sn, void* stream) {
   gpa_clear_error();
   if (rows < 0 || C < 0) {
-    gpa_set_error("gpa_residual_layernorm_bf16: negative size");
+    gpa_set_error("%s: negative size", fn);
     return GPA_E_INVALID;
   }
   if (C % 512 != 0 || C < 512 || C > 4096) {
-    gpa_set_error("gpa_residual_layernorm_bf16: C=%lld unsupported (multiple of 512, <= 4096)",
-                  (long long)C);
+    gpa_set_error("%s: C=%lld unsupported (multiple of 512, <= 4096)", fn, (long long)C);
     return GPA_E_UNSUPPORTED;
   }
   if (rows == 0) return GPA_OK;
   if (!x || (y && !gamma) || (ln_out && (!ln_weight || !ln_bias)) || (!h_out && !ln_out) ||
       (h_out && !y)) {
-    gpa_set_error("gpa_residual_layernorm_bf16: null pointer (x; gamma with y; weight and bias "
-                  "with ln_out; an output; h_out only with y)");
+    gpa_set_error("%s: null pointer (x; gamma with y; weight and bias with ln_out; an output; "
+                  "h_out only with y)", fn);
     return GPA_E_INVALID;
   }
   if (!(eps >= 0.f) || !isfinite(eps)) {
-    gpa_set_error("gpa_residual_layernorm_bf16: eps must be finite and >= 0");
+    gpa_set_error("%s: eps must be finite and >= 0", fn);
     return GPA_E_INVALID;
   }
   auto al16 = [](const void* p) { return (uintptr_t)p % 16 == 0; };
@@ -163,12 +170,12 @@ extern "C" int gpa_residual_layernorm_bf16(const void* x, const void* y, const v
                        (!y || rows == 1 || y_sn % 8 == 0) && (!h_out || rows == 1 || h_sn % 8 == 0) &&
                        (!ln_out || rows == 1 || ln_sn % 8 == 0);
   if (!aligned) {
-    gpa_set_error("gpa_residual_layernorm_bf16: rows and parameters must be 16-byte aligned");
+    gpa_set_error("%s: rows and parameters must be 16-byte aligned", fn);
     return GPA_E_INVALID;
   }
   const int64_t blocks = (rows + kRowsPerWG - 1) / kRowsPerWG;
   if (blocks > 0x7fffffff) {
-    gpa_set_error("gpa_residual_layernorm_bf16: too many rows");
+    gpa_set_error("%s: too many rows", fn);
     return GPA_E_UNSUPPORTED;
   }
   LnArgs a{};
@@ -185,19 +192,34 @@ extern "C" int gpa_residual_layernorm_bf16(const void* x, const void* y, const v
   const dim3 grid((unsigned)blocks), block(64 * kRowsPerWG);
   const hipStream_t s = (hipStream_t)stream;
   switch (C / 512) {
-    case 1: hipLaunchKernelGGL(residual_layernorm_kernel<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(residual_layernorm_kernel<2>, grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL(residual_layernorm_kernel<3>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(residual_layernorm_kernel<4>, grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL(residual_layernorm_kernel<5>, grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL(residual_layernorm_kernel<6>, grid, block, 0, s, a); break;
-    case 7: hipLaunchKernelGGL(residual_layernorm_kernel<7>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(residual_layernorm_kernel<8>, grid, block, 0, s, a); break;
+#define GPA_LN_CASE(nc) \
+  case nc: hipLaunchKernelGGL((residual_layernorm_kernel<nc, F16>), grid, block, 0, s, a); break;
+    GPA_LN_CASE(1) GPA_LN_CASE(2) GPA_LN_CASE(3) GPA_LN_CASE(4)
+    GPA_LN_CASE(5) GPA_LN_CASE(6) GPA_LN_CASE(7)
+#undef GPA_LN_CASE
+    default: hipLaunchKernelGGL((residual_layernorm_kernel<8, F16>), grid, block, 0, s, a); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_residual_layernorm_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+#define GPA_LN_ARGS                                                                          \
+  const void *x, const void *y, const void *gamma, const void *ln_weight, const void *ln_bias, \
+      float eps, int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn, void *h_out,           \
+      int64_t h_sn, void *ln_out, int64_t ln_sn, void *stream
+#define GPA_LN_PASS \
+  x, y, gamma, ln_weight, ln_bias, eps, rows, C, x_sn, y_sn, h_out, h_sn, ln_out, ln_sn, stream
+
+extern "C" int gpa_residual_layernorm_bf16(GPA_LN_ARGS) {
+  return ln_run<false>("gpa_residual_layernorm_bf16", GPA_LN_PASS);
+}
+
+extern "C" int gpa_residual_layernorm_f16(GPA_LN_ARGS) {
+  return ln_run<true>("gpa_residual_layernorm_f16", GPA_LN_PASS);
 }

@@ -84,6 +84,9 @@ __device__ __forceinline__ float group_sum8(float v) {
   return v;
 }
 
+// F16: the projection and the 16-bit outputs are fp16 (the fp16-autocast
+// stack) instead of bf16; the arithmetic is the same fp32.
+template <bool F16>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
   // Lane group g owns slice 32*blockIdx.y + g (q heads, then k heads) for
   // the kTokens tokens of blockIdx.x; groups past 2H load the last slice
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
     const uint32_t b = row / N, n = row - b * N;
     float x[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = (float)xv[r][i];
+    for (int i = 0; i < 8; ++i) x[i] = half_to_f32<F16>(xv[r][i]);
 
     float s = 0.f;
 #pragma unroll
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
     } else {
       bf16x8 yv;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) yv[i] = (__bf16)x[i];
+      for (int i = 0; i < 8; ++i) yv[i] = f32_to_half<F16>(x[i]);
       __builtin_nontemporal_store(__builtin_bit_cast(u32x4, yv),
                                   reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + o));
     }
@@ -174,35 +177,39 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(QkArgs a) {
 
 using namespace gpa;
 
-extern "C" int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H,
-                                     int64_t D, int64_t qkv_sb, int64_t qkv_sn,
-                                     int64_t k_offset, const float* ln_weight,
-                                     const float* ln_bias, float eps, const int32_t* pos,
-                                     int64_t period, const float* rope_cs, int64_t npos,
-                                     void* q_out, int q_dtype, void* k_out, int k_dtype,
-                                     void* stream) {
+namespace {
+
+// Shared by the bf16 and fp16 entry points (F16 selects the 16-bit format of
+// the projection and of 16-bit outputs); `fn` names the entry point in error
+// messages.
+template <bool F16>
+int qk_run(const char* fn, const void* qkv, int64_t B, int64_t N, int64_t H, int64_t D,
+           int64_t qkv_sb, int64_t qkv_sn, int64_t k_offset, const float* ln_weight,
+           const float* ln_bias, float eps, const int32_t* pos, int64_t period,
+           const float* rope_cs, int64_t npos, void* q_out, int q_dtype, void* k_out,
+           int k_dtype, void* stream) {
   gpa_clear_error();
   if (B < 0 || N < 0 || H < 0) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: negative size");
+    gpa_set_error("%s: negative size", fn);
     return GPA_E_INVALID;
   }
   if (D != kHeadDim) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: head dim %lld is not implemented (64 only)",
-                  (long long)D);
+    gpa_set_error("%s: head dim %lld is not implemented (64 only)", fn, (long long)D);
     return GPA_E_UNSUPPORTED;
   }
   if (B == 0 || N == 0 || H == 0) return GPA_OK;
   if (!qkv || !ln_weight || !ln_bias || !q_out || !k_out) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: null pointer");
+    gpa_set_error("%s: null pointer", fn);
     return GPA_E_INVALID;
   }
   if (pos != nullptr && (period <= 0 || rope_cs == nullptr || npos <= 0 || npos > (1 << 20))) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: rotation needs period > 0, a table and 0 < npos <= 2^20");
+    gpa_set_error("%s: rotation needs period > 0, a table and 0 < npos <= 2^20", fn);
     return GPA_E_INVALID;
   }
+  const int half = F16 ? GPA_DTYPE_F16 : GPA_DTYPE_BF16;
   for (int dt : {q_dtype, k_dtype}) {
-    if (dt != GPA_DTYPE_F32 && dt != GPA_DTYPE_BF16) {
-      gpa_set_error("gpa_qk_norm_rope_bf16: output dtype %d is not fp32 or bf16", dt);
+    if (dt != GPA_DTYPE_F32 && dt != half) {
+      gpa_set_error("%s: output dtype %d is not fp32 or %s", fn, dt, F16 ? "fp16" : "bf16");
       return GPA_E_UNSUPPORTED;
     }
   }
@@ -210,12 +217,12 @@ extern "C" int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int6
                        (uintptr_t)k_out % 16 == 0 && (B == 1 || qkv_sb % 8 == 0) &&
                        (N == 1 || qkv_sn % 8 == 0) && k_offset % 8 == 0 && k_offset >= H * D;
   if (!aligned) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: rows must be 16-byte aligned and k must follow q "
-                  "(k_offset >= H*64, multiple of 8)");
+    gpa_set_error("%s: rows must be 16-byte aligned and k must follow q (k_offset >= H*64, "
+                  "multiple of 8)", fn);
     return GPA_E_INVALID;
   }
   if (2 * H > 65535) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: too many heads");
+    gpa_set_error("%s: too many heads", fn);
     return GPA_E_UNSUPPORTED;
   }
   QkArgs a{};
@@ -229,15 +236,34 @@ extern "C" int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int6
   const int64_t blocks = (a.rows + kTokens - 1) / kTokens;
   const int64_t sblocks = (2 * H + kSlicesPerBlock - 1) / kSlicesPerBlock;
   if (a.rows > 0xffffffffLL - kTokens || blocks > 0x7fffffff || period > 0x7fffffff) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: problem exceeds the grid limit");
+    gpa_set_error("%s: problem exceeds the grid limit", fn);
     return GPA_E_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)blocks, (unsigned)sblocks),
+  hipLaunchKernelGGL(qk_norm_rope_kernel<F16>, dim3((unsigned)blocks, (unsigned)sblocks),
                      dim3(kThreads), 0, (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_qk_norm_rope_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+#define GPA_QK_ARGS                                                                          \
+  const void *qkv, int64_t B, int64_t N, int64_t H, int64_t D, int64_t qkv_sb, int64_t qkv_sn, \
+      int64_t k_offset, const float *ln_weight, const float *ln_bias, float eps,              \
+      const int32_t *pos, int64_t period, const float *rope_cs, int64_t npos, void *q_out,    \
+      int q_dtype, void *k_out, int k_dtype, void *stream
+#define GPA_QK_PASS                                                                          \
+  qkv, B, N, H, D, qkv_sb, qkv_sn, k_offset, ln_weight, ln_bias, eps, pos, period, rope_cs,  \
+      npos, q_out, q_dtype, k_out, k_dtype, stream
+
+extern "C" int gpa_qk_norm_rope_bf16(GPA_QK_ARGS) {
+  return qk_run<false>("gpa_qk_norm_rope_bf16", GPA_QK_PASS);
+}
+
+extern "C" int gpa_qk_norm_rope_f16(GPA_QK_ARGS) {
+  return qk_run<true>("gpa_qk_norm_rope_f16", GPA_QK_PASS);
 }

@@ -225,9 +225,10 @@ class GpaAttention(nn.Module):
         """q, k, v [B, H, N, D] from the block input (attention.py:210-220).
 
         With qk LayerNorm the normalisation, the rotation and the cast run
-        as one `gpa::qk_norm_rope` kernel over the bf16 projection (q bf16;
-        k fp32 when `k_f32`, for the K merge, else bf16); v stays a view of
-        the projection.  Without it (the patch embedder's blocks) q, k, v
+        as one `gpa::qk_norm_rope` kernel over the bf16 (or, under fp16
+        autocast, fp16) projection (q in the projection's format; k fp32
+        when `k_f32`, for the K merge, else the projection's format); v
+        stays a view of the projection.  Without it (the patch embedder's blocks) q, k, v
         are all views of the projection.
         """
         B, N, C = x.shape
@@ -235,9 +236,9 @@ class GpaAttention(nn.Module):
         qkv = self.qkv(x)
         v = qkv.view(B, N, 3, H, D)[:, :, 2].transpose(1, 2)
         if isinstance(self.q_norm, nn.LayerNorm):
-            if qkv.dtype != torch.bfloat16:
-                raise ValueError("the fused qk-norm/RoPE kernel takes a bf16 projection "
-                                 "(run the bf16 model under autocast)")
+            if qkv.dtype not in (torch.bfloat16, torch.float16):
+                raise ValueError("the fused qk-norm/RoPE kernel takes a bf16 or fp16 "
+                                 "projection (run the model under bf16 or fp16 autocast)")
             ln_w = torch.stack((self.q_norm.weight, self.k_norm.weight))
             ln_b = torch.stack((self.q_norm.bias, self.k_norm.bias))
             q, k = torch.ops.gpa.qk_norm_rope(
@@ -404,19 +405,20 @@ class Block(nn.Module):
         self.ls2 = LayerScale(dim, ls_init)
 
     def _fused_ok(self, x: torch.Tensor) -> bool:
-        """The fused kernel reproduces the bf16 chain: a bf16 block on a bf16
-        stream, under bf16 autocast or none."""
-        if not (self.attn.cfg.fused_norms and x.is_cuda and x.dtype == torch.bfloat16
-                and x.shape[-1] % 512 == 0 and self.norm1.weight.dtype == torch.bfloat16
-                and self.ls1.gamma.dtype == torch.bfloat16):
+        """The fused kernel reproduces the 16-bit chain: a bf16 (fp16) block
+        on a bf16 (fp16) stream, under autocast to that format or none."""
+        dt = x.dtype
+        if not (self.attn.cfg.fused_norms and x.is_cuda and dt in (torch.bfloat16, torch.float16)
+                and x.shape[-1] % 512 == 0 and self.norm1.weight.dtype == dt
+                and self.ls1.gamma.dtype == dt):
             return False
-        return (not torch.is_autocast_enabled("cuda")
-                or torch.get_autocast_dtype("cuda") == torch.bfloat16)
+        return not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") == dt
 
     def forward(self, x, rope: Optional[RopeTable] = None, global_merging=None):
         if self._fused_ok(x):
             # block.py:84-96 with the elementwise steps fused: LayerNorm 1 to
-            # bf16; x + ls1(attn) with LayerNorm 2 in one pass; x + ls2(mlp).
+            # the 16-bit format; x + ls1(attn) with LayerNorm 2 in one pass;
+            # x + ls2(mlp).
             rl = torch.ops.gpa.residual_layernorm
             _, ln1 = rl(x, None, None, self.norm1.weight, self.norm1.bias, self.norm1.eps, False)
             a = self.attn(ln1, rope, global_merging)

@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 10
+ABI_VERSION = 12
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -119,6 +119,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, ctypes.c_int, _vp, ctypes.c_int,  # q_out, q_dtype, k_out, k_dtype
         _vp,                           # stream
     ]
+    lib.gpa_qk_norm_rope_f16.restype = ctypes.c_int
+    lib.gpa_qk_norm_rope_f16.argtypes = lib.gpa_qk_norm_rope_bf16.argtypes
     lib.gpa_pool_shared_bf16.restype = ctypes.c_int
     lib.gpa_pool_shared_bf16.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp,  # k, v, pooled_k, pooled_v, size, assign
@@ -141,6 +143,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _vp, _i64, _vp, _i64,          # h_out, h_sn, ln_out, ln_sn
         _vp,                           # stream
     ]
+    lib.gpa_residual_layernorm_f16.restype = ctypes.c_int
+    lib.gpa_residual_layernorm_f16.argtypes = lib.gpa_residual_layernorm_bf16.argtypes
     lib.gpa_merge_heads.restype = ctypes.c_int
     lib.gpa_merge_heads.argtypes = [
         _vp, ctypes.c_int, _vp,        # t, dtype, out
@@ -179,7 +183,8 @@ def exported_symbols() -> Tuple[str, ...]:
             "gpa_merge_heads", "gpa_lse_combine_bf16", "gpa_qk_norm_rope_bf16",
             "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
             "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16",
-            "gpa_attn_keybias_bf16_noalloc", "gpa_lse_combine_f16")
+            "gpa_attn_keybias_bf16_noalloc", "gpa_lse_combine_f16", "gpa_qk_norm_rope_f16",
+            "gpa_residual_layernorm_f16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -499,16 +504,17 @@ def qk_norm_rope(qkv: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, eps:
                  pos: Optional[torch.Tensor], rope_cs: Optional[torch.Tensor], heads: int,
                  q_f32: bool, k_f32: bool) -> Tuple[torch.Tensor, torch.Tensor]:
     """qk LayerNorm + 2D RoPE of the QKV projection qkv [B, N, >= 3*heads*64]
-    (bf16): returns q, k [B, heads, N, 64] (fp32 or bf16 each).
+    (bf16 or fp16): returns q, k [B, heads, N, 64], each fp32 or of qkv's
+    16-bit format.
 
     ln_w / ln_b [2, 64]: the q and k LayerNorm affine parameters; pos
     [period, 2] int32 (token n uses row n mod period) and rope_cs
     [npos, 16, 2] fp32 (cos, sin) tables, or both None for no rotation.
     """
     dev = _require_gpu(qkv, ln_w, ln_b)
-    if qkv.dtype != torch.bfloat16 or qkv.dim() != 3:
-        raise ValueError(f"gpa::qk_norm_rope: qkv must be bf16 [B, N, 3C], got {qkv.dtype} "
-                         f"{tuple(qkv.shape)}")
+    if qkv.dtype not in (torch.bfloat16, torch.float16) or qkv.dim() != 3:
+        raise ValueError(f"gpa::qk_norm_rope: qkv must be bf16 or fp16 [B, N, 3C], got "
+                         f"{qkv.dtype} {tuple(qkv.shape)}")
     H = int(heads)
     if H <= 0 or qkv.shape[2] < 3 * H * 64:
         raise ValueError(f"gpa::qk_norm_rope: rows of {qkv.shape[2]} cannot hold q, k, v of "
@@ -531,18 +537,21 @@ def qk_norm_rope(qkv: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, eps:
     if not _rows_ok(qkv, 8):
         qkv = qkv.contiguous()
     B, N, _ = qkv.shape
-    q = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if q_f32 else torch.bfloat16)
-    k = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if k_f32 else torch.bfloat16)
+    f16 = qkv.dtype == torch.float16
+    half, half_code = (torch.float16, GPA_DTYPE_F16) if f16 else (torch.bfloat16, GPA_DTYPE_BF16)
+    q = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if q_f32 else half)
+    k = torch.empty(B, H, N, 64, device=dev, dtype=torch.float32 if k_f32 else half)
     if q.numel() == 0:
         return q, k
     with torch.cuda.device(dev):
-        rc = lib().gpa_qk_norm_rope_bf16(
+        fn = lib().gpa_qk_norm_rope_f16 if f16 else lib().gpa_qk_norm_rope_bf16
+        rc = fn(
             qkv.data_ptr(), B, N, H, 64, _st(qkv, 0), _rs(qkv, 1), H * 64,
             w.data_ptr(), bb.data_ptr(), float(eps),
             pos.data_ptr() if pos is not None else None, period,
             rope_cs.data_ptr() if rope_cs is not None else None, npos,
-            q.data_ptr(), GPA_DTYPE_F32 if q_f32 else GPA_DTYPE_BF16,
-            k.data_ptr(), GPA_DTYPE_F32 if k_f32 else GPA_DTYPE_BF16, _stream(dev))
+            q.data_ptr(), GPA_DTYPE_F32 if q_f32 else half_code,
+            k.data_ptr(), GPA_DTYPE_F32 if k_f32 else half_code, _stream(dev))
     _check(rc, "gpa::qk_norm_rope")
     return q, k
 
@@ -550,8 +559,9 @@ def qk_norm_rope(qkv: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, eps:
 @qk_norm_rope.register_fake
 def _qk_norm_rope_fake(qkv, ln_w, ln_b, eps, pos, rope_cs, heads, q_f32, k_f32):
     B, N, _ = qkv.shape
-    return (qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if q_f32 else torch.bfloat16),
-            qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if k_f32 else torch.bfloat16))
+    half = qkv.dtype if qkv.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    return (qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if q_f32 else half),
+            qkv.new_empty(B, heads, N, 64, dtype=torch.float32 if k_f32 else half))
 
 
 @torch.library.custom_op("gpa::pool_shared", mutates_args=())
@@ -672,14 +682,17 @@ def _merge_metric_fake(metric, proj, order, mode):
 def residual_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], gamma: Optional[torch.Tensor],
                        weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float,
                        want_h: bool) -> Tuple[torch.Tensor, torch.Tensor]:
-    """h = bf16(x + bf16(gamma * y)) (h = x without y) and LayerNorm(h) in
-    bf16, over the last dim of bf16 x / y.  Returns (h if want_h else an
-    empty tensor, LayerNorm(h) if weight is given else an empty tensor)."""
+    """h = r(x + r(gamma * y)) (h = x without y) and LayerNorm(h), rounded
+    (r) to x's 16-bit format, over the last dim of x / y; all tensors bf16, or
+    all fp16.  Returns (h if want_h else an empty tensor, LayerNorm(h) if
+    weight is given else an empty tensor)."""
     dev = _require_gpu(*[t for t in (x, y, gamma, weight, bias) if t is not None])
     C = x.shape[-1]
-    for name, t in (("x", x), ("y", y), ("gamma", gamma), ("weight", weight), ("bias", bias)):
-        if t is not None and t.dtype != torch.bfloat16:
-            raise ValueError(f"gpa::residual_layernorm takes bf16 {name}, got {t.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"gpa::residual_layernorm takes bf16 or fp16 x, got {x.dtype}")
+    for name, t in (("y", y), ("gamma", gamma), ("weight", weight), ("bias", bias)):
+        if t is not None and t.dtype != x.dtype:
+            raise ValueError(f"gpa::residual_layernorm: {name} is {t.dtype}, x is {x.dtype}")
     if y is not None and (y.shape != x.shape or gamma is None or gamma.shape != (C,)):
         raise ValueError("gpa::residual_layernorm: y must match x and gamma be [C]")
     if weight is not None and (bias is None or weight.shape != (C,) or bias.shape != (C,)):
@@ -698,13 +711,15 @@ def residual_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], gamma: Option
     if weight is not None:
         weight, bias = weight.contiguous(), bias.contiguous()
     rows = xr.shape[0]
-    h = torch.empty(x.shape, device=dev, dtype=torch.bfloat16) if want_h else x.new_empty(0)
-    ln = torch.empty(x.shape, device=dev, dtype=torch.bfloat16) if weight is not None \
+    h = torch.empty(x.shape, device=dev, dtype=x.dtype) if want_h else x.new_empty(0)
+    ln = torch.empty(x.shape, device=dev, dtype=x.dtype) if weight is not None \
         else x.new_empty(0)
     if rows == 0:
         return h, ln
     with torch.cuda.device(dev):
-        rc = lib().gpa_residual_layernorm_bf16(
+        fn = (lib().gpa_residual_layernorm_f16 if x.dtype == torch.float16
+              else lib().gpa_residual_layernorm_bf16)
+        rc = fn(
             xr.data_ptr(), None if yr is None else yr.data_ptr(),
             None if gamma is None else gamma.data_ptr(),
             None if weight is None else weight.data_ptr(),

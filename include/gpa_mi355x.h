@@ -16,14 +16,14 @@
  *                           merging/merge.py:234-250).
  *   gpa_lse_combine_bf16  — merge of two partial attentions by their log2
  *                           LSE (replaces vggt/layers/attention.py:166-176).
- *   gpa_qk_norm_rope_bf16 — qk LayerNorm + 2D RoPE + cast of a block's
+ *   gpa_qk_norm_rope_bf16 (and _f16) — qk LayerNorm + 2D RoPE + cast of a block's
  *                           attention operands (replaces the torch op
  *                           sequence of vggt/layers/attention.py:210-220).
  *   gpa_pool_shared_bf16  — pooled summaries of the frame-special shared
  *                           K/V set (replaces vggt/layers/attention.py:113-140).
  *   gpa_merge_metric_bf16 — the merge's metric projection, normalisation and
  *                           dst/src split (replaces merging/merge.py:180-187).
- *   gpa_residual_layernorm_bf16 — residual + LayerScale + LayerNorm of the
+ *   gpa_residual_layernorm_bf16 (and _f16) — residual + LayerScale + LayerNorm of the
  *                           caller's blocks (replaces vggt/layers/block.py:84-96
  *                           torch ops).
  *
@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 10
+#define GPA_ABI_VERSION 12
 
 enum {
   GPA_OK = 0,
@@ -277,6 +277,17 @@ int gpa_qk_norm_rope_bf16(const void* qkv, int64_t B, int64_t N, int64_t H, int6
                           const float* rope_cs, int64_t npos,
                           void* q_out, int q_dtype, void* k_out, int k_dtype, void* stream);
 
+/* The same on an fp16 projection (the fp16-autocast stack): q_dtype /
+ * k_dtype GPA_DTYPE_F32 or GPA_DTYPE_F16; the arithmetic is the same fp32.
+ * Replaces the same reference lines under fp16 autocast (the cast of
+ * fused_attention.py:139-144 then goes to fp16). */
+int gpa_qk_norm_rope_f16(const void* qkv, int64_t B, int64_t N, int64_t H, int64_t D,
+                         int64_t qkv_sb, int64_t qkv_sn, int64_t k_offset,
+                         const float* ln_weight, const float* ln_bias, float eps,
+                         const int32_t* pos, int64_t period,
+                         const float* rope_cs, int64_t npos,
+                         void* q_out, int q_dtype, void* k_out, int k_dtype, void* stream);
+
 /*
  * Pooled summaries of the frame-special shared K/V set.  For every
  * (b, h, frame s) and its patch keys x_p = k[b, h, s*P + pts + p, :]
@@ -347,6 +358,15 @@ int gpa_residual_layernorm_bf16(const void* x, const void* y, const void* gamma,
                                 int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn,
                                 void* h_out, int64_t h_sn, void* ln_out, int64_t ln_sn,
                                 void* stream);
+
+/* The same on fp16 rows and parameters: the chain under fp16 autocast on an
+ * fp16 model (the reference's accuracy-evaluation stack, eval/eval_co3d.py:
+ * 152 and :226), every bf16 rounding above an fp16 rounding. */
+int gpa_residual_layernorm_f16(const void* x, const void* y, const void* gamma,
+                               const void* ln_weight, const void* ln_bias, float eps,
+                               int64_t rows, int64_t C, int64_t x_sn, int64_t y_sn,
+                               void* h_out, int64_t h_sn, void* ln_out, int64_t ln_sn,
+                               void* stream);
 
 #ifdef __cplusplus
 }

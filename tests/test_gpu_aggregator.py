@@ -199,43 +199,53 @@ def test_frame_special_block_attention_matches_reference(dev, kp, gh, gw):
     _compare(got, _proj_ref(blk, out), f"frame-special block (kp {kp}, {gh} x {gw})")
 
 
-@pytest.mark.parametrize("hw", [(518, 518), (392, 518)])
-def test_small_aggregator_runs_every_global_path(dev, hw):
+@pytest.mark.parametrize("hw,dt", [((518, 518), torch.bfloat16), ((392, 518), torch.bfloat16),
+                                   ((518, 518), torch.float16)])
+def test_small_aggregator_runs_every_global_path(dev, hw, dt):
+    """Every global path (frame-special pooling, merged, core merged) on
+    square and rectangular images, as the bf16 benchmark stack and as the
+    fp16 accuracy-evaluation stack (fp16 model under fp16 autocast,
+    eval/eval_co3d.py:226 and :152): finite outputs of the DPT shapes in the
+    model's dtype, bit-identical on a second forward."""
     cfg = A.GpaConfig(depth=3, vit_depth=1, early_frame_split=1, merging=1,
                       core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2),
                       img_size=hw[0], img_width=hw[1])
     assert [cfg.block_kind(i) for i in range(3)] == ["frame_special", "merged", "merged"]
     P = cfg.tokens_per_frame
-    model = A.build_aggregator(cfg, device=dev, seed=2)
-    imgs = A.shifted_texture_images(FRAMES, size=hw, device=dev).to(torch.bfloat16)
+    model = A.build_aggregator(cfg, device=dev, dtype=dt, seed=2)
+    imgs = A.shifted_texture_images(FRAMES, size=hw, device=dev).to(dt)
     tracer = A.StageTimer()
     model.set_tracer(tracer)
     tracer.start()
-    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+    with torch.no_grad(), torch.autocast("cuda", dtype=dt):
         outs = model(imgs)
+        again = model(imgs)
+    assert all(torch.equal(a, b) for a, b in zip(outs, again))
     stages = tracer.totals()
     assert {"frame_special_attn", "pool", "merge", "merged_attn", "frame_attn"} <= set(stages)
     assert len(outs) == 3
     for o in outs:
-        assert o.shape == (1, FRAMES, P, 2048) and o.dtype == torch.bfloat16
+        assert o.shape == (1, FRAMES, P, 2048) and o.dtype == dt
         assert torch.isfinite(o).all()
     flops = A.aggregator_flops(cfg, FRAMES)
     assert flops["similarity"] > 0 and flops["global_attn"] > 0
 
 
-@pytest.mark.parametrize("frames,k_f32", [(3, True), (2, False)])
-def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32):
-    """gpa::qk_norm_rope against LayerNorm + rotate-half RoPE in fp64."""
+@pytest.mark.parametrize("frames,k_f32,half", [(3, True, torch.bfloat16), (2, False, torch.bfloat16),
+                                               (3, True, torch.float16), (2, False, torch.float16)])
+def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32, half):
+    """gpa::qk_norm_rope against LayerNorm + rotate-half RoPE in fp64, on a
+    bf16 and an fp16 projection (16-bit outputs in the projection's format)."""
     g = torch.Generator(device=dev).manual_seed(frames)
     N = frames * P
-    qkv = (torch.randn(1, N, 3 * 1024, generator=g, device=dev) * 1.5 + 0.3).bfloat16()
+    qkv = (torch.randn(1, N, 3 * 1024, generator=g, device=dev) * 1.5 + 0.3).to(half)
     ln_w = 1 + 0.3 * torch.randn(2, 64, generator=g, device=dev)
     ln_b = 0.2 * torch.randn(2, 64, generator=g, device=dev)
     pos1 = A.frame_positions(GRID, PTS, dev)
     rope = A.Rope2D(100.0).table(pos1, 64)
     q, k = torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, rope.pos, rope.cs, 16, False, k_f32)
-    assert q.dtype == torch.bfloat16 and q.shape == (1, 16, N, 64)
-    assert k.dtype == (torch.float32 if k_f32 else torch.bfloat16)
+    assert q.dtype == half and q.shape == (1, 16, N, 64)
+    assert k.dtype == (torch.float32 if k_f32 else half)
     x = qkv.cpu().double().view(1, N, 3, 16, 64).permute(2, 0, 3, 1, 4)
     pos = pos1.cpu().repeat(frames, 1)
     for got, t, i in ((q, x[0], 0), (k, x[1], 1)):
@@ -244,7 +254,8 @@ def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32):
         y = (t - mu) / torch.sqrt(var + 1e-5) * ln_w[i].cpu().double() + ln_b[i].cpu().double()
         want = _rope_ref(y, pos).double()
         err = (got.cpu().double() - want).abs()
-        bound = (2.0 ** -8 if got.dtype == torch.bfloat16 else 1e-5) * want.abs() + 1e-5
+        rel = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}.get(got.dtype, 1e-5)
+        bound = rel * want.abs() + 1e-5
         assert (err <= bound).all(), f"max err {err.max().item():.3e}"
     # no rotation: plain LayerNorm
     q0, _ = torch.ops.gpa.qk_norm_rope(qkv, ln_w, ln_b, 1e-5, None, None, 16, True, True)

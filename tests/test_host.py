@@ -177,12 +177,13 @@ def test_merge_empty_is_a_no_op():
     assert _merge(S=0) == _native.GPA_OK
 
 
-def _qk(**kw):
+def _qk(f16=False, **kw):
     args = dict(qkv=FAKE, B=1, N=10, H=2, D=64, sb=3840, sn=384, koff=128, w=FAKE, b=FAKE,
-                eps=1e-5, pos=FAKE, period=5, cs=FAKE, npos=8, q=FAKE, qd=1, k=FAKE, kd=0,
-                stream=None)
+                eps=1e-5, pos=FAKE, period=5, cs=FAKE, npos=8, q=FAKE, qd=2 if f16 else 1,
+                k=FAKE, kd=0, stream=None)
     args.update(kw)
-    return _native.lib().gpa_qk_norm_rope_bf16(*args.values())
+    fn = _native.lib().gpa_qk_norm_rope_f16 if f16 else _native.lib().gpa_qk_norm_rope_bf16
+    return fn(*args.values())
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -201,6 +202,17 @@ def _qk(**kw):
 def test_qk_norm_rope_argument_errors(kw, code):
     assert _qk(**kw) == code
     assert _native.lib().gpa_last_error()
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(qd=1), _native.GPA_E_UNSUPPORTED),                # bf16 output from the fp16 entry
+    (dict(kd=1), _native.GPA_E_UNSUPPORTED),
+    (dict(D=32), _native.GPA_E_UNSUPPORTED),
+    (dict(sn=380), _native.GPA_E_INVALID),
+])
+def test_qk_norm_rope_f16_argument_errors(kw, code):
+    assert _qk(f16=True, **kw) == code
+    assert b"gpa_qk_norm_rope_f16" in _native.lib().gpa_last_error()
 
 
 def test_qk_norm_rope_empty_is_a_no_op():
