@@ -14,7 +14,9 @@
 // This is the `_pool` of vggt/layers/attention.py:113-140 under bf16
 // autocast: the normalised keys and seeds enter the einsum (:130) in bf16,
 // its scores come back in bf16, argmax takes the first maximum, and the
-// sums run in fp32 (scatter_add_, :132-139) before the cast back.  The
+// sums run in fp32 (scatter_add_, :132-139) before the cast back.  The fp16
+// instantiation is the same under fp16 autocast on fp16 keys and values
+// (fp16 normalised rows, fp16 MFMA, scores rounded to fp16).  The
 // reference sums with atomics in a run-dependent order; here every sum has
 // a fixed order, so the means are deterministic.
 //
@@ -68,12 +70,17 @@ constexpr int kStage = 32 + 8;
 // Row stride of the partial-sum buffer (32 features + 1 of padding).
 constexpr int kRed = 33;
 
-__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
+// A score rounded to the 16-bit format, as the autocast einsum returns it.
+template <bool F16>
+__device__ __forceinline__ float round16(float x) { return half_to_f32<F16>(f32_to_half<F16>(x)); }
+// 1.0 in the 16-bit format: the one-hot A operand.
+template <bool F16>
+constexpr uint32_t kOne16 = F16 ? 0x3c00u : 0x3f80u;
 
 // NSB: blocks of 32 seeds (1 or 2), so the accumulators of an absent block
 // take no registers.  One block fits three waves per SIMD without spills
 // (158 VGPRs), 8 % faster than two; two blocks stay at two (spills at three).
-template <int NSB>
+template <int NSB, bool F16>
 __global__ __launch_bounds__(kPoolThreads) __attribute__((amdgpu_waves_per_eu(NSB == 1 ? 3 : 1)))
 void pool_shared_kernel(PoolArgs a) {
   __shared__ int count[kMaxPool];
@@ -106,12 +113,15 @@ void pool_shared_kernel(PoolArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf((float)r[ks][e], (float)r[ks][e], ss);
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(r[ks][e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
     const float inv = 1.0f / fmaxf(__builtin_sqrtf(sum_halves(ss)), 1e-6f);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) nb[ks][e] = (__bf16)((float)r[ks][e] * inv);
+      for (int e = 0; e < 8; ++e) nb[ks][e] = f32_to_half<F16>(half_to_f32<F16>(r[ks][e]) * inv);
   };
 
   // Seed blocks: block sb holds seeds 32sb .. 32sb+31 in lane rows l32 (zero
@@ -146,11 +156,11 @@ void pool_shared_kernel(PoolArgs a) {
     for (int sb = 0; sb < NSB; ++sb) {
       f32x16 sc = {};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sc = mfma32x32x16(seed[sb][ks], xb[ks], sc);
+      for (int ks = 0; ks < 4; ++ks) sc = mfma32x32x16_t<F16>(seed[sb][ks], xb[ks], sc);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {           // seeds in increasing order
         const int g = sb * 32 + mfma_row(r, hi);
-        const float v = bf16_round(sc[r]);
+        const float v = round16<F16>(sc[r]);
         if (g < a.npool && v > best) {
           best = v;
           bi = g;
@@ -198,10 +208,10 @@ void pool_shared_kernel(PoolArgs a) {
           for (int q = 0; q < 4; ++q) {
             const uint32_t w = q < 2 ? ab.x : ab.y;
             const uint32_t b0 = (w >> (16 * (q & 1))) & 0xffu, b1 = (w >> (16 * (q & 1) + 8)) & 0xffu;
-            oh[q] = (b0 == id ? 0x3f80u : 0u) | (b1 == id ? 0x3f800000u : 0u);   // bf16 1.0
+            oh[q] = (b0 == id ? kOne16<F16> : 0u) | (b1 == id ? kOne16<F16> << 16 : 0u);
           }
-          acc[fh][sb] = mfma32x32x16(__builtin_bit_cast(bf16x8, oh), __builtin_bit_cast(bf16x8, bx),
-                                     acc[fh][sb]);
+          acc[fh][sb] = mfma32x32x16_t<F16>(__builtin_bit_cast(bf16x8, oh),
+                                            __builtin_bit_cast(bf16x8, bx), acc[fh][sb]);
         }
       }
     }
@@ -221,7 +231,8 @@ void pool_shared_kernel(PoolArgs a) {
         const int g = e >> 5, f = e & 31;
         const float sum = ((red[0][g][f] + red[1][g][f]) + red[2][g][f]) + red[3][g][f];
         const float inv = 1.0f / fmaxf((float)count[g], 1.0f);
-        out[(out_row0 + g) * kPoolD + 32 * fh + f] = __builtin_bit_cast(uint16_t, (__bf16)(sum * inv));
+        out[(out_row0 + g) * kPoolD + 32 * fh + f] =
+            __builtin_bit_cast(uint16_t, f32_to_half<F16>(sum * inv));
       }
       __syncthreads();
     }
@@ -259,35 +270,39 @@ void pool_shared_kernel(PoolArgs a) {
 
 using namespace gpa;
 
-extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* pooled_v,
-                                    float* size, int32_t* assign, int64_t B, int64_t H,
-                                    int64_t S, int64_t P, int64_t pts, int64_t grid_h,
-                                    int64_t grid_w, int64_t kp, int64_t D, int64_t k_sb,
-                                    int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh,
-                                    int64_t v_sn, void* stream) {
+namespace {
+
+// Shared by the bf16 and fp16 entry points; `fn` names the entry point in
+// error messages.
+template <bool F16>
+int pool_run(const char* fn, const void* k, const void* v, void* pooled_k, void* pooled_v,
+             float* size, int32_t* assign, int64_t B, int64_t H, int64_t S, int64_t P,
+             int64_t pts, int64_t grid_h, int64_t grid_w, int64_t kp, int64_t D, int64_t k_sb,
+             int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+             void* stream) {
   gpa_clear_error();
   if (B < 0 || H < 0 || S < 0 || P < 0 || pts < 0 || grid_h < 0 || grid_w < 0 || kp <= 0) {
-    gpa_set_error("gpa_pool_shared_bf16: negative size or kp <= 0");
+    gpa_set_error("%s: negative size or kp <= 0", fn);
     return GPA_E_INVALID;
   }
   if (D != kPoolD) {
-    gpa_set_error("gpa_pool_shared_bf16: head dim %lld unsupported (64 only)", (long long)D);
+    gpa_set_error("%s: head dim %lld unsupported (64 only)", fn, (long long)D);
     return GPA_E_UNSUPPORTED;
   }
   if (B == 0 || H == 0 || S == 0 || grid_h == 0 || grid_w == 0) return GPA_OK;
   if (!k || !v || !pooled_k || !pooled_v || !size) {
-    gpa_set_error("gpa_pool_shared_bf16: null pointer");
+    gpa_set_error("%s: null pointer", fn);
     return GPA_E_INVALID;
   }
   if (P < pts + grid_h * grid_w) {
-    gpa_set_error("gpa_pool_shared_bf16: frame of %lld tokens cannot hold %lld specials and a "
-                  "%lldx%lld patch grid", (long long)P, (long long)pts, (long long)grid_h,
+    gpa_set_error("%s: frame of %lld tokens cannot hold %lld specials and a "
+                  "%lldx%lld patch grid", fn, (long long)P, (long long)pts, (long long)grid_h,
                   (long long)grid_w);
     return GPA_E_INVALID;
   }
   const int64_t nh = (grid_h + kp - 1) / kp, nw = (grid_w + kp - 1) / kp;
   if (nh * nw > kMaxPool || grid_h * grid_w > kMaxPatches) {
-    gpa_set_error("gpa_pool_shared_bf16: %lld seeds / %lld patches exceed the kernel's 64 / 4096",
+    gpa_set_error("%s: %lld seeds / %lld patches exceed the kernel's 64 / 4096", fn,
                   (long long)(nh * nw), (long long)(grid_h * grid_w));
     return GPA_E_UNSUPPORTED;
   }
@@ -296,13 +311,13 @@ extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k
                        (H == 1 || (k_sh % 8 == 0 && v_sh % 8 == 0)) && k_sn % 8 == 0 &&
                        v_sn % 8 == 0 && k_sn >= D && v_sn >= D;
   if (!aligned) {
-    gpa_set_error("gpa_pool_shared_bf16: k and v rows must be 16-byte aligned, unit feature "
-                  "stride");
+    gpa_set_error("%s: k and v rows must be 16-byte aligned, unit feature "
+                  "stride", fn);
     return GPA_E_INVALID;
   }
   const int64_t groups = B * H * S;
   if (groups > 0x7fffffff) {
-    gpa_set_error("gpa_pool_shared_bf16: too many groups");
+    gpa_set_error("%s: too many groups", fn);
     return GPA_E_UNSUPPORTED;
   }
   PoolArgs a{};
@@ -318,15 +333,34 @@ extern "C" int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k
   a.gh = (int)grid_h; a.gw = (int)grid_w;
   a.kp = (int)kp; a.nw = (int)nw; a.npool = (int)(nh * nw);
   if (a.npool > 32)
-    hipLaunchKernelGGL(pool_shared_kernel<2>, dim3((unsigned)groups), dim3(kPoolThreads), 0,
+    hipLaunchKernelGGL((pool_shared_kernel<2, F16>), dim3((unsigned)groups), dim3(kPoolThreads), 0,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(pool_shared_kernel<1>, dim3((unsigned)groups), dim3(kPoolThreads), 0,
+    hipLaunchKernelGGL((pool_shared_kernel<1, F16>), dim3((unsigned)groups), dim3(kPoolThreads), 0,
                        (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    gpa_set_error("gpa_pool_shared_bf16: launch failed: %s", hipGetErrorString(e));
+    gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
   return GPA_OK;
+}
+
+}  // namespace
+
+#define GPA_POOL_ARGS                                                                         \
+  const void *k, const void *v, void *pooled_k, void *pooled_v, float *size, int32_t *assign, \
+      int64_t B, int64_t H, int64_t S, int64_t P, int64_t pts, int64_t grid_h, int64_t grid_w, \
+      int64_t kp, int64_t D, int64_t k_sb, int64_t k_sh, int64_t k_sn, int64_t v_sb,          \
+      int64_t v_sh, int64_t v_sn, void *stream
+#define GPA_POOL_PASS                                                                         \
+  k, v, pooled_k, pooled_v, size, assign, B, H, S, P, pts, grid_h, grid_w, kp, D, k_sb, k_sh, \
+      k_sn, v_sb, v_sh, v_sn, stream
+
+extern "C" int gpa_pool_shared_bf16(GPA_POOL_ARGS) {
+  return pool_run<false>("gpa_pool_shared_bf16", GPA_POOL_PASS);
+}
+
+extern "C" int gpa_pool_shared_f16(GPA_POOL_ARGS) {
+  return pool_run<true>("gpa_pool_shared_f16", GPA_POOL_PASS);
 }

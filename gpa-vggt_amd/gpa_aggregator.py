@@ -346,7 +346,7 @@ def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, gri
     Returns (pooled_k, pooled_v [B, H, S*npool, D], size [B, H, S, npool]
     fp32, assign [B, H, S, grid_h*grid_w] or an empty tensor)."""
     npool = -(-grid_h // kp) * -(-grid_w // kp)
-    if npool <= POOL_KERNEL_MAX_SEEDS and k.dtype == torch.bfloat16:
+    if npool <= POOL_KERNEL_MAX_SEEDS and k.dtype in (torch.bfloat16, torch.float16):
         return torch.ops.gpa.pool_shared(k, v, frames, pts, grid_h, grid_w, kp, want_assign)
     B, H, N, D = k.shape
     P = N // frames

@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -129,6 +129,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64, _i64, _i64,  # k strides, v strides
         _vp,                           # stream
     ]
+    lib.gpa_pool_shared_f16.restype = ctypes.c_int
+    lib.gpa_pool_shared_f16.argtypes = lib.gpa_pool_shared_bf16.argtypes
     lib.gpa_merge_metric_bf16.restype = ctypes.c_int
     lib.gpa_merge_metric_bf16.argtypes = [
         _vp, ctypes.c_int,             # metric, metric dtype
@@ -184,7 +186,7 @@ def exported_symbols() -> Tuple[str, ...]:
             "gpa_pool_shared_bf16", "gpa_merge_metric_bf16", "gpa_sim_argmax_f16",
             "gpa_attn_keybias_f16", "gpa_residual_layernorm_bf16",
             "gpa_attn_keybias_bf16_noalloc", "gpa_lse_combine_f16", "gpa_qk_norm_rope_f16",
-            "gpa_residual_layernorm_f16")
+            "gpa_residual_layernorm_f16", "gpa_pool_shared_f16")
 
 
 def _check(rc: int, what: str) -> None:
@@ -569,15 +571,15 @@ def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid_h:
                 grid_w: int, kp: int, want_assign: bool
                 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Pooled summaries of the frame-special shared set from k, v [B, H, S*P, 64]
-    (bf16) on a grid_h x grid_w patch grid: returns pooled k, v
-    [B, H, S*npool, 64] bf16, size [B, H, S, npool] fp32 and, if asked, the
+    (both bf16 or both fp16) on a grid_h x grid_w patch grid: returns pooled
+    k, v [B, H, S*npool, 64] in that format, size [B, H, S, npool] fp32 and, if asked, the
     assignment [B, H, S, grid_h*grid_w] int32 (else empty);
     npool = ceil(grid_h/kp) * ceil(grid_w/kp)."""
     dev = _require_gpu(k, v)
     for name, t in (("k", k), ("v", v)):
-        if t.dtype != torch.bfloat16 or t.dim() != 4:
-            raise ValueError(f"gpa::pool_shared: {name} must be bf16 [B,H,N,64], got {t.dtype} "
-                             f"{tuple(t.shape)}")
+        if t.dtype not in (torch.bfloat16, torch.float16) or t.dim() != 4 or t.dtype != k.dtype:
+            raise ValueError(f"gpa::pool_shared: {name} must be bf16 or fp16 [B,H,N,64] like k, "
+                             f"got {t.dtype} {tuple(t.shape)}")
     if k.shape != v.shape:
         raise ValueError(f"gpa::pool_shared: k {tuple(k.shape)} and v {tuple(v.shape)} differ")
     if kp <= 0 or grid_h < 0 or grid_w < 0:
@@ -592,15 +594,16 @@ def pool_shared(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid_h:
         k = k.contiguous()
     if not _rows_ok(v, 8):
         v = v.contiguous()
-    pk = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
-    pv = torch.empty(B, H, S * npool, D, device=dev, dtype=torch.bfloat16)
+    pk = torch.empty(B, H, S * npool, D, device=dev, dtype=k.dtype)
+    pv = torch.empty(B, H, S * npool, D, device=dev, dtype=k.dtype)
     size = torch.empty(B, H, S, npool, device=dev, dtype=torch.float32)
     assign = (torch.empty(B, H, S, grid_h * grid_w, device=dev, dtype=torch.int32)
               if want_assign else torch.empty(0, device=dev, dtype=torch.int32))
     if pk.numel() == 0:
         return pk, pv, size, assign
     with torch.cuda.device(dev):
-        rc = lib().gpa_pool_shared_bf16(
+        fn = lib().gpa_pool_shared_f16 if k.dtype == torch.float16 else lib().gpa_pool_shared_bf16
+        rc = fn(
             k.data_ptr(), v.data_ptr(), pk.data_ptr(), pv.data_ptr(), size.data_ptr(),
             assign.data_ptr() if want_assign else None, B, H, S, P, pts, grid_h, grid_w, kp, D,
             _st(k, 0), _st(k, 1), _rs(k, 2), _st(v, 0), _st(v, 1), _rs(v, 2), _stream(dev))

@@ -19,7 +19,7 @@
  *   gpa_qk_norm_rope_bf16 (and _f16) — qk LayerNorm + 2D RoPE + cast of a block's
  *                           attention operands (replaces the torch op
  *                           sequence of vggt/layers/attention.py:210-220).
- *   gpa_pool_shared_bf16  — pooled summaries of the frame-special shared
+ *   gpa_pool_shared_bf16 (and _f16) — pooled summaries of the frame-special shared
  *                           K/V set (replaces vggt/layers/attention.py:113-140).
  *   gpa_merge_metric_bf16 — the merge's metric projection, normalisation and
  *                           dst/src split (replaces merging/merge.py:180-187).
@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 12
+#define GPA_ABI_VERSION 13
 
 enum {
   GPA_OK = 0,
@@ -316,6 +316,14 @@ int gpa_pool_shared_bf16(const void* k, const void* v, void* pooled_k, void* poo
                          int64_t P, int64_t pts, int64_t grid_h, int64_t grid_w, int64_t kp,
                          int64_t D, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                          int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream);
+
+/* The same on fp16 k and v (the pooling under fp16 autocast: fp16
+ * normalised rows and fp16 scores; fp16 pooled outputs). */
+int gpa_pool_shared_f16(const void* k, const void* v, void* pooled_k, void* pooled_v,
+                        float* size, int32_t* assign, int64_t B, int64_t H, int64_t S,
+                        int64_t P, int64_t pts, int64_t grid_h, int64_t grid_w, int64_t kp,
+                        int64_t D, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                        int64_t v_sb, int64_t v_sh, int64_t v_sn, void* stream);
 
 /*
  * Front end of the bipartite merge: for every batch b and output row j,

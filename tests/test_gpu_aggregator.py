@@ -364,6 +364,50 @@ def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     assert torch.equal(pk3, pk) and torch.equal(pv3, pv)
 
 
+@pytest.mark.parametrize("gh,gw,kp", [(37, 37, 8), (28, 37, 5)])
+def test_pool_shared_kernel_fp16(dev, gh, gw, kp):
+    """The fp16 instantiation (the pooling under fp16 autocast): assignment
+    equal to the fp64 argmax over fp16-rounded normalised rows wherever the
+    top two scores are more than two fp16 steps apart, exact sizes, fp16
+    means within 2^-11 relative of fp64 means over the kernel's own
+    assignment, and the torch restatement under fp16 autocast agreeing on
+    the sure rows."""
+    g = torch.Generator(device=dev).manual_seed(gh + gw + kp)
+    B, H, S = 1, 4, 3
+    P_ = PTS + gh * gw
+    npatch = gh * gw
+    k = (torch.randn(B, H, S * P_, 64, generator=g, device=dev) * 0.7).half()
+    v = torch.randn(B, H, S * P_, 64, generator=g, device=dev).half()
+    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, True)
+    assert pk.dtype == pv.dtype == torch.float16
+    npool = -(-gh // kp) * -(-gw // kp)
+    kp5 = k.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+    vp5 = v.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+
+    def nh(t):
+        t = t.float()
+        return (t / t.norm(dim=-1, keepdim=True).clamp_min(1e-6)).half().double()
+    G = kp5.shape[0]
+    seeds = kp5.view(G, gh, gw, 64)[:, ::kp, ::kp].reshape(G, -1, 64)
+    sc = torch.einsum("gpd,gsd->gps", nh(kp5), nh(seeds))
+    top2 = sc.topk(2, dim=-1).values
+    sure = (top2[..., 0] - top2[..., 1]) > 2 * 2.0 ** -11
+    a = assign.cpu().long().reshape(-1, npatch)
+    assert sure.float().mean() > 0.5
+    assert torch.equal(a[sure], sc.argmax(-1)[sure])
+    onehot = torch.nn.functional.one_hot(a, npool).double()
+    cnt = onehot.sum(1)
+    assert torch.equal(size.cpu().reshape(-1, npool).double(), cnt)
+    for got, rows in ((pk, kp5), (pv, vp5)):
+        want = torch.einsum("gps,gpd->gsd", onehot, rows.double()) / cnt.clamp_min(1)[..., None]
+        err = (got.cpu().double().reshape(-1, npool, 64) - want).abs()
+        assert (err <= 2.0 ** -11 * want.abs() + 1e-6).all(), f"max err {err.max().item():.3e}"
+    with torch.autocast("cuda", dtype=torch.float16):
+        _, _, _, a_t = A.pool_shared_torch(k.view(B, H, S, P_, 64), v.view(B, H, S, P_, 64),
+                                           PTS, gh, gw, kp)
+    assert torch.equal(a_t.cpu().reshape(-1, npatch)[sure], a[sure])
+
+
 def test_pool_shared_batches_and_strided_k(dev):
     """B = 2 with batch strides of a head-major view (k and v sliced out of a
     [B, 2H, N, 64] buffer, heads 1, 3, 5, 7): each (batch, head, frame) equals
