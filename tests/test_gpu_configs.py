@@ -201,3 +201,42 @@ def test_config5_aggregator_200_frames(dev, aggregator):
     for r1, r2 in zip(log1, log2):
         key = "size" if r1["kind"] == "merged" else "pool_size"
         assert torch.equal(r1[key], r2[key])
+
+
+def test_config5_fp16_evaluation_stack(dev):
+    """The same 200-frame aggregator as the reference's accuracy evaluation
+    runs it (eval/eval_co3d.py:152, 226): the fp16 model under fp16
+    autocast, reference defaults.  Every stage runs its fp16 kernel twin;
+    finite fp16 outputs of the DPT shapes, bit-identical on a second forward,
+    and the merge and pooling invariants of the bf16 run."""
+    cfg = A.GpaConfig()
+    f16 = torch.float16
+    agg = A.build_aggregator(cfg, device=dev, dtype=f16, seed=0)
+    frames = 200
+    N = frames * P
+    imgs = A.shifted_texture_images(frames, device=dev).to(f16)
+    logs = ([], [])
+    outs = []
+    for i, log in enumerate(logs):
+        print(f"[config 5, fp16] forward {i + 1} of 2 on {frames} frames", flush=True)
+        agg.set_merge_log(log)
+        with torch.no_grad(), torch.autocast("cuda", dtype=f16):
+            outs.append(agg(imgs))
+        agg.set_merge_log(None)
+        torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert a.shape == (1, frames, P, 2 * cfg.embed_dim) and a.dtype == f16
+        assert torch.isfinite(a).all()
+        assert torch.equal(a, b), "the fp16 aggregator is not bit-reproducible"
+    merged = [r for r in logs[0] if r["kind"] == "merged"]
+    assert [r["block"] for r in merged] == list(range(9, 24))
+    for r in merged:
+        assert r["size"].sum().item() == N and r["size"].min().item() >= 1
+    assert {r["keys"] for r in merged} == {66_845, 219_840}
+    pools = [r for r in logs[0] if r["kind"] == "pool"]
+    assert len(pools) == 9
+    for r in pools:
+        assert torch.equal(r["pool_size"].sum(-1),
+                           torch.full((1, 16, frames), float(GRID * GRID), device=dev))
+    del agg
+    torch.cuda.empty_cache()
