@@ -15,7 +15,8 @@ kernels and their caller (noheat61/GPA-VGGT):
                  fp64 brute-force K/V mean     (pins merge.heads)
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
-`bench.py` may import it, and only as the checker or the timed CPU baseline.
+`bench.py` may import it, and only as the reference the results are
+compared against or as the timed CPU baseline.
 The product (`gpa-vggt_amd/merging`) never imports it and has no CPU path.
 
 Every function here is pinned by a check in `tests/test_oracle_*.py`
