@@ -276,6 +276,20 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
 // keeps each iteration's work inside it.  One barrier per iteration recycles
 // the slots of the tiles just read; tiles past the split end read as zeros
 // and are masked in the last epilogue.
+// max(a, b, c, d) of four scores, NaN operands dropped (IEEE mode), as
+// v_max3_f32 + v_max_f32.  Written as asm because the compiler's fmaxf first
+// quiets every operand it cannot prove to be a computed value (an MFMA result
+// is not one), which doubles the instruction count.  The operands are scores
+// the MFMAs of the previous pipeline iteration (or the prologue) produced,
+// more than a sched_barrier and a workgroup barrier earlier, or selects of
+// them, so no MFMA-to-VALU read hazard can fall on these instructions.
+__device__ __forceinline__ float max4_scores(float a, float b, float c, float d) {
+  float m3, m4;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(m3) : "v"(a), "v"(b), "v"(c));
+  asm("v_max_f32 %0, %1, %2" : "=v"(m4) : "v"(m3), "v"(d));
+  return m4;
+}
+
 constexpr int kPipeRing = 8;                 // 16-row tile slots
 constexpr int kPipePairsAhead = kPipeRing / 2 - 1;
 
@@ -317,16 +331,19 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
                              : bf16x8{};
   }
 
-  float best[kSB][4];
-  int bt[kSB][4];
+  // Per source block: the running max over the lane's four destination
+  // rows of every tile so far, the first tile reaching it, and that tile's
+  // four scores (to find the row inside it at the end).
+  float best[kSB], keep[kSB][4];
+  int bt[kSB];
   const int tile0 = (int)(n_begin >> 4);
 #pragma unroll
-  for (int sb = 0; sb < kSB; ++sb)
+  for (int sb = 0; sb < kSB; ++sb) {
+    best[sb] = -INFINITY;
+    bt[sb] = tile0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      best[sb][r] = -INFINITY;
-      bt[sb][r] = tile0;
-    }
+    for (int r = 0; r < 4; ++r) keep[sb][r] = -INFINITY;
+  }
 
   const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + 15) / 16) : 0;
   const int npairs = (ntiles + 1) / 2;
@@ -359,21 +376,31 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
       for (int sb = 0; sb < kSB; ++sb) acc[sb] = mfma16x16x32_t<F16>(af, sf[sb][ks], acc[sb]);
     }
   };
-  // Running max / first tile reaching it, per slot (strict >: an earlier
-  // tile keeps a tie).  MASKED: rows at or past the split end never win.
+  // Running max / first tile reaching it (strict >: an earlier tile keeps a
+  // tie), over the tile's max of the lane's four rows: v_max3 + v_max and one
+  // compare and six selects per four scores instead of a compare and two
+  // selects per score (296 instead of 392 VALU per 128 MFMAs).  NaN scores
+  // never win: v_max3/v_max drop NaN operands, a tile whose four are all NaN
+  // yields NaN, and NaN > best is false.  MASKED: rows at or past the split
+  // end never win.
   auto epilogue = [&](const f32x4 (&acc)[kSB], int tile_rel, auto masked) {
     const int tile = tile0 + tile_rel;
 #pragma unroll
-    for (int sb = 0; sb < kSB; ++sb)
+    for (int sb = 0; sb < kSB; ++sb) {
+      float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float v = acc[sb][r];
-        bool upd = v > best[sb][r];
+        v[r] = acc[sb][r];
         if constexpr (decltype(masked)::value)
-          upd = upd && (n_begin + (int64_t)tile_rel * 16 + 4 * quad + r < n_end);
-        best[sb][r] = upd ? v : best[sb][r];
-        bt[sb][r] = upd ? tile : bt[sb][r];
+          v[r] = n_begin + (int64_t)tile_rel * 16 + 4 * quad + r < n_end ? v[r] : -INFINITY;
       }
+      const float m4 = max4_scores(v[0], v[1], v[2], v[3]);
+      const bool upd = m4 > best[sb];
+      best[sb] = upd ? m4 : best[sb];
+      bt[sb] = upd ? tile : bt[sb];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) keep[sb][r] = upd ? v[r] : keep[sb][r];
+    }
   };
 
   f32x4 cur[2][kSB], nxt[2][kSB];
@@ -383,9 +410,11 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
 #pragma unroll
       for (int sb = 0; sb < kSB; ++sb) asm volatile("" : "+v"(nxt[u][sb]));
 #pragma unroll
-    for (int sb = 0; sb < kSB; ++sb)
+    for (int sb = 0; sb < kSB; ++sb) {
+      asm volatile("" : "+v"(best[sb]), "+v"(bt[sb]));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(best[sb][r]), "+v"(bt[sb][r]));
+      for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(keep[sb][r]));
+    }
   };
 
   if (npairs > 0) {
@@ -448,16 +477,21 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
 
 #pragma unroll
   for (int sb = 0; sb < kSB; ++sb) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    // The first of the best tile's rows holding the max (-inf rows that never
+    // beat the initial -inf: the split's first row).
+    // The value reported is the score at that row (so a -0 / +0 tie reports
+    // the first row's sign, as a per-score running max would).
+    float bv = best[sb];
+    int r_best = 0;
+    bool found = false;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float v = best[sb][r];
-      const int idx = bt[sb][r] * 16 + 4 * quad + r;
-      const bool take = v > bv || (v == bv && idx < bi);
-      bv = take ? v : bv;
-      bi = take ? idx : bi;
+      const bool hit = !found && keep[sb][r] == bv;
+      r_best = hit ? r : r_best;
+      bv = hit ? keep[sb][r] : bv;
+      found = found || hit;
     }
+    int bi = bt[sb] * 16 + 4 * quad + r_best;
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
       const float ov = __shfl_xor(bv, sh);
