@@ -111,6 +111,7 @@ struct AttnArgs {
   int64_t lse_sb, lse_sh;
   uint32_t k_bytes, v_bytes, rec_bytes;  // extent of one (batch, head) slice
   float c;                                // sm_scale * log2(e)
+  int o16;                                // O rows 16-byte aligned (16-byte stores)
 };
 
 struct RecArgs {
@@ -372,25 +373,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
 
   // Q^T as the B-operand of S^T = K . Q^T: in block j the lane supplies
-  // query q_base + 32 j, features 16*ks + 8*hi .. +8.  |q| feeds the bound.
+  // query q_base + 32 j, features 16*ks + 8*hi .. +8.  Only the loads here:
+  // |q| (for the bound) is formed after the prologue's tile DMAs are issued,
+  // so that both blocks' Q loads and the first tiles are in flight together.
+  // Formed right after each block's loads, it made the compiler wait for
+  // them before issuing anything else: three memory round trips in a row
+  // before the first tile (about 3 us of a 48 us own-frame workgroup).
   bf16x8 qf[kBlk][4];
   float q_norm[kBlk];
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
     const int64_t row = q_base + 32 * j;
-    float ss = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < 4; ++ks)
       qf[j][ks] = row < p.M ? *reinterpret_cast<const bf16x8*>(Q + row * p.q_sm + ks * 16 + hi * 8)
                             : bf16x8{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = half_to_f32<F16>(qf[j][ks][e]);
-        ss = __builtin_fmaf(f, f, ss);
-      }
-    }
-    q_norm[j] = __builtin_sqrtf(sum_halves(ss));
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(K, p.k_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, p.v_bytes);
@@ -572,9 +571,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     return;
   }
 
-  // Prologue: tiles 0 .. kMainAhead-1 in flight; S(0) and the certification.
+  // Prologue: tiles 0 .. kMainAhead-1 in flight behind the Q loads; |q|;
+  // S(0) and the certification.
 #pragma unroll
   for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < kBlk; ++j) {
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(qf[j][ks][e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
+    q_norm[j] = __builtin_sqrtf(sum_halves(ss));
+  }
   wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
   tile_barrier();
   scores(*ring[0], s_cur);
@@ -675,26 +688,65 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   // Drain the DMAs still in flight before the workgroup can exit.
   wait_vm<0>();
 
-  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+  // O goes through LDS so that every store writes whole 128-byte rows:
+  // eight rows of 16 bytes per lane per instruction instead of 8 bytes in
+  // each of 32 rows (the strided stores took ~2 us per workgroup to issue).
+  // Wave w stages its 64 rows in ring slot w (8 KB of its 8.25 KB), free once
+  // every wave has drained its DMAs (the barrier).  Row r of the wave (block
+  // r / 32, query row r % 32) keeps its 16-byte chunk c at chunk c ^ (r & 7):
+  // the writes of one instruction meet at most two to a bank, the row reads
+  // not at all.  A wave's LDS operations run in order, so the reads need no
+  // further barrier.
+  tile_barrier();
+  MainTile& slot_w = wave == 0 ? ring0 : wave == 1 ? ring1 : wave == 2 ? ring2 : ring3;
+  uint16_t* const stage = reinterpret_cast<uint16_t*>(&slot_w);
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
-    const int64_t row = q_base + 32 * j;
+    const int r = 32 * j + l32;
     const float l_tot = sum_halves(l_acc[j][0]);
     const float inv = 1.0f / l_tot;
-    if (row < p.M) {
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + 8 * g + 4 * hi;
-          const bf16x4 ov = {f32_to_half<F16>(o_acc[j][db][4 * g + 0] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 1] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 2] * inv),
-                             f32_to_half<F16>(o_acc[j][db][4 * g + 3] * inv)};
-          *reinterpret_cast<bf16x4*>(O + row * p.o_sm + d0) = ov;
-        }
-      if (p.lse && hi == 0)
-        p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_off[j] + __log2f(l_tot);
+      for (int g = 0; g < 4; ++g) {
+        const int cw = db * 4 + g;
+        const bf16x4 ov = {f32_to_half<F16>(o_acc[j][db][4 * g + 0] * inv),
+                           f32_to_half<F16>(o_acc[j][db][4 * g + 1] * inv),
+                           f32_to_half<F16>(o_acc[j][db][4 * g + 2] * inv),
+                           f32_to_half<F16>(o_acc[j][db][4 * g + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(&stage[r * kHD + ((cw ^ (r & 7)) << 3) + 4 * hi]) = ov;
+      }
+    const int64_t row = q_base + 32 * j;
+    if (p.lse && hi == 0 && row < p.M)
+      p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_off[j] + __log2f(l_tot);
+  }
+  // All eight row reads first, then the stores (read-wait-store in turn
+  // serialised eight LDS round trips).
+  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+  const int64_t row0 = (int64_t)qb * kQPerWG + wave * kQPerWave;
+  const int ch = lane & 7;
+  constexpr int kRowSets = kQPerWave / 8;
+  u32x4 ov16[kRowSets];
+#pragma unroll
+  for (int i = 0; i < kRowSets; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    ov16[i] = *reinterpret_cast<const u32x4*>(&stage[r * kHD + ((ch ^ (r & 7)) << 3)]);
+  }
+  if (p.o16) {
+#pragma unroll
+    for (int i = 0; i < kRowSets; ++i) {
+      const int64_t row = row0 + 8 * i + (lane >> 3);
+      if (row < p.M) *reinterpret_cast<u32x4*>(O + row * p.o_sm + ch * 8) = ov16[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRowSets; ++i) {
+      const int64_t row = row0 + 8 * i + (lane >> 3);
+      if (row < p.M) {
+        u32x2* dst = reinterpret_cast<u32x2*>(O + row * p.o_sm + ch * 8);
+        dst[0] = u32x2{ov16[i][0], ov16[i][1]};
+        dst[1] = u32x2{ov16[i][2], ov16[i][3]};
+      }
     }
   }
 }
@@ -872,6 +924,7 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   p.v_bytes = (uint32_t)(((N - 1) * v_sn + D) * 2);
   p.rec_bytes = (uint32_t)(ntiles * kRec * sizeof(float));
   p.c = c;
+  p.o16 = ((uintptr_t)o % 16 == 0 && o_sm % 8 == 0 && o_sb % 8 == 0 && o_sh % 8 == 0) ? 1 : 0;
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
   hipLaunchKernelGGL(attn_main_kernel<F16>, grid, block, 0, s, p);
