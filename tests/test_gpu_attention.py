@@ -203,6 +203,49 @@ def test_rows_past_n_never_reach_the_output(dev, N):
     assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
 
 
+def _abi_attention(q, k, v, b, o, lse):
+    """gpa_attn_keybias_bf16 through the C ABI with the caller's o and lse."""
+    import ctypes
+    L = _native.lib()
+    B, H, M, D = q.shape
+    N = k.shape[2]
+    ws = torch.empty(L.gpa_attn_keybias_workspace_bytes(B, H, M, N), dtype=torch.uint8,
+                     device=q.device)
+    st = lambda t: (t.stride(0), t.stride(1), t.stride(2))
+    rc = L.gpa_attn_keybias_bf16(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(), _native.GPA_BIAS_F32,
+        b.stride(0), b.stride(1), b.stride(3), o.data_ptr(), lse.data_ptr(), B, H, M, N, D,
+        *st(q), *st(k), *st(v), *st(o), lse.stride(0), lse.stride(1), ws.data_ptr(), ws.numel(),
+        ctypes.c_float(0.125), torch.cuda.current_stream(q.device).cuda_stream)
+    assert rc == _native.GPA_OK, L.gpa_last_error()
+
+
+@pytest.mark.parametrize("o_row", [72, 68])
+def test_strided_output_rows(dev, o_row):
+    """o written into rows of o_row elements (the output is the first 64 of
+    each): 72 keeps the rows 16-byte aligned (whole-row 16-byte stores), 68
+    only 8-byte aligned (the same rows stored as 8-byte halves).  Both must
+    equal the contiguous output bit for bit and leave the gap columns and the
+    rows past M untouched.  M = 700 leaves a partly live and an empty wave in
+    the last workgroup of each batch-head."""
+    B, H, M, N = 2, 3, 700, 333
+    q, k, v, b = _inputs(B, H, M, N, seed=o_row, bias="f32")
+    q, k, v, b = q.to(dev), k.to(dev), v.to(dev), b.to(dev)
+    o_ref = torch.empty(B, H, M, 64, device=dev, dtype=torch.bfloat16)
+    lse_ref = torch.empty(B, H, M, device=dev)
+    _abi_attention(q, k, v, b, o_ref, lse_ref)
+    sentinel = -7.0
+    buf = torch.full((B, H, M + 5, o_row), sentinel, device=dev, dtype=torch.bfloat16)
+    o = buf[:, :, :M, :64]
+    lse = torch.empty(B, H, M, device=dev)
+    _abi_attention(q, k, v, b, o, lse)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o_ref.float()).all()
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse.view(torch.int32), lse_ref.view(torch.int32))
+    assert (buf[:, :, :, 64:] == sentinel).all() and (buf[:, :, M:, :] == sentinel).all()
+
+
 def test_fp32_inputs_follow_the_cast_contract(dev):
     q, k, v, b = _inputs(1, 2, 100, 130, seed=8, bias="f32")
     q32, k32, v32 = q.float().to(dev), k.float().to(dev), v.float().to(dev)
