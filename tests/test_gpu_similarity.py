@@ -113,15 +113,15 @@ def test_rows_past_n_never_win(dev, M, N):
     assert np.array_equal(vidx[sure], fidx[sure])
 
 
-@pytest.mark.parametrize("D", [96, 128, 512])
-def test_nan_and_zero_rows(dev, D):
+@pytest.mark.parametrize("D,half", [(96, False), (128, False), (512, False), (128, True)])
+def test_nan_and_zero_rows(dev, D, half):
     """NaN scores never win (the strict > of fused_similarity.py:73 over
     tl.max's NaN-free maximum): a source row of NaN features scores NaN
     against everything and yields -inf with index 0; destination rows
     holding a NaN are never chosen; an all-zero source row scores 0 against
     every other row and takes index 0.  Covers the register-staged (D 96),
-    pipelined (D 128) and GEMM-tiled (D 512) kernels, with several
-    destination splits."""
+    pipelined (D 128, bf16 and fp16 operands) and GEMM-tiled (D 512)
+    kernels, with several destination splits."""
     M, N = 600, 3000
     a = _unit_bf16_values((1, M, D), seed=71 + D)
     b = _unit_bf16_values((1, N, D), seed=72 + D)
@@ -132,7 +132,11 @@ def test_nan_and_zero_rows(dev, D):
     a[0, nan_src] = float("nan")
     a[0, zero_src] = 0.0
     b[0, nan_dst, D // 2] = float("nan")
-    vmax, vidx = fused_similarity_argmax(a.to(dev), b.to(dev))
+    if half:        # fp16 holds these bf16 values to < 1e-7 (only tiny ones lose bits)
+        vmax, vidx = fused_similarity_argmax(a.half().to(dev), b.half().to(dev))
+        vmax = vmax.float()                  # returned in fp16, the input format
+    else:
+        vmax, vidx = fused_similarity_argmax(a.to(dev), b.to(dev))
     vmax, vidx = vmax[0].cpu(), vidx[0].cpu()
     assert torch.all(vmax[nan_src] == -float("inf")) and torch.all(vidx[nan_src] == 0)
     assert torch.all(vmax[zero_src] == 0) and torch.all(vidx[zero_src] == 0)
@@ -143,7 +147,7 @@ def test_nan_and_zero_rows(dev, D):
     rows[nan_src] = False
     rows[zero_src] = False
     fmax, fidx, gap = sim_argmax_fp64(a[:, rows], b[:, keep])
-    assert np.abs(vmax[rows].numpy() - fmax[0]).max() < 1e-5
+    assert np.abs(vmax[rows].numpy() - fmax[0]).max() < (1e-3 if half else 1e-5)
     sure = gap[0] > 1e-5
     kept = torch.nonzero(keep)[:, 0].numpy()
     assert np.array_equal(vidx[rows].numpy()[sure], kept[fidx[0]][sure])
