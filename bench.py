@@ -9,8 +9,10 @@ algorithmic TFLOP/s (2*M*N*D for the similarity, 4*BH*M*N*D for attention).
 The JSON line also carries per-kernel ms / TFLOP/s / % of the bf16 dense
 MFMA peak (the reference 200-frame shapes, the unprojected 1024-d
 similarity, the frame-special calls, the HBM-bound kernels around the path,
-the fp16 twins, and sharp-logit attention with the share of waves on the
-lazily moved softmax offset), the end-to-end latency of one GPA block (100
+the fp16 twins, and attention on larger logits -- LayerNorm-scale and sharp
+q/k -- with the shares of waves on the tile-0 and the lazily moved softmax
+offsets), the practical MFMA ceiling (a hipBLASLt bf16 GEMM on random and on
+all-zero data), the end-to-end latency of one GPA block (100
 frames) and of the whole aggregator (200 frames) on the random-init VGGT-1B
 harness for the GPA schedule and for vanilla VGGT, the roofline of the
 dominant kernel and a CPU baseline (the torch restatement of the reference
@@ -143,9 +145,8 @@ def e2e_latency(dev) -> dict:
     del vm
     torch.cuda.empty_cache()
     # The accuracy-evaluation stack of the reference (eval_co3d.py:152, 226):
-    # the fp16 model under fp16 autocast, reference defaults.  The fused
-    # residual + LayerNorm kernel is bf16-only, so those steps run as torch
-    # ops here; every other kernel has its fp16 twin.
+    # the fp16 model under fp16 autocast, reference defaults; every kernel
+    # runs as its fp16 twin.
     f16 = torch.float16
     fm = A.build_aggregator(cfg, device=dev, dtype=f16)
     imgs16 = imgs.to(f16)
@@ -154,8 +155,15 @@ def e2e_latency(dev) -> dict:
         with torch.no_grad(), torch.autocast("cuda", dtype=f16):
             return fm(imgs16)
     ms, peak = A.timed(run16, warmup=1, iters=2)
+    tracer = A.StageTimer()
+    fm.set_tracer(tracer)
+    tracer.start()
+    run16()
+    stages = tracer.totals()
+    fm.set_tracer(None)
     res["aggregator_200f_fp16_eval_stack"] = {
         "ms": round(ms, 1), "peak_gib": round(peak, 2), "protocol": "1 warm-up call, mean of 2",
+        "stages_ms": {k: round(v, 2) for k, v in sorted(stages.items(), key=lambda kv: -kv[1])},
         "workload": "reference defaults, fp16 model under fp16 autocast (eval_co3d.py:152, 226)"}
     log(f"[bench] aggregator 200 frames (fp16 evaluation stack): {ms:.1f} ms")
     del fm, imgs16, imgs
@@ -446,16 +454,20 @@ def main(argv=None) -> int:
         kernels["attn_keybias_f16_16h_274800x68700"] = kernel_entry(f_attn, t)
         del qh, kh, vh, bh
         log("[bench] fp16 shapes done")
-        # Sharp logits: q and k scaled up so the Cauchy-Schwarz score bound
-        # sits far above the rows' real scores and waves fall back from the
-        # certified fixed softmax offset to the lazily moved one (same
-        # workload otherwise).  lazy_waves_pct is read from the kernel's
-        # per-wave flags.
-        for dt, scale in ((torch.bfloat16, 40.0), (torch.float16, 6.0), (torch.float16, 12.0)):
+        # Larger logits: q and k scaled up so the Cauchy-Schwarz score bound
+        # sits above what the bound-certified softmax offset covers, and
+        # waves take the tile-0 offset (verified after the loop) or the
+        # lazily moved one (same workload otherwise).  x8 puts the features
+        # at LayerNorm scale (unit variance, as the model's qk norm leaves
+        # them), where fp16's 16-unit window no longer certifies most rows.
+        # The shares come from the kernel's per-wave flags.
+        for dt, scale in ((torch.bfloat16, 8.0), (torch.float16, 8.0), (torch.bfloat16, 40.0),
+                          (torch.float16, 6.0), (torch.float16, 12.0)):
             qs, ks = (q.float() * scale).to(dt), (k.float() * scale).to(dt)
             vs, bs = v.to(dt), bias.to(dt)
             _, _, flags = _native.attn_keybias_offset_flags(qs, ks, vs, bs, SM_SCALE)
-            lazy = float(flags.float().mean().item())
+            fl = flags.view(q.shape[1], -1)[:, :-(-q.shape[2] // 64)]     # waves holding queries
+            share = lambda bit: round(100 * float(((fl & bit) != 0).float().mean().item()), 2)  # noqa: E731
             fn = lambda: attention_keybias(qs, ks, vs, bs, SM_SCALE)  # noqa: E731
             fn()
             t = statistics.median(event_ms(fn, 3))
@@ -463,11 +475,40 @@ def main(argv=None) -> int:
             entry = kernel_entry(f_attn, t)
             base = attn_ms if dt == torch.bfloat16 else \
                 kernels["attn_keybias_f16_16h_274800x68700"]["ms"]
-            entry.update({"qk_scale": scale, "lazy_waves_pct": round(100 * lazy, 2),
+            entry.update({"qk_scale": scale,
+                          "tile0_offset_waves_pct": share(_native.ATTN_FLAG_TILE0),
+                          "lazy_waves_pct": share(_native.ATTN_FLAG_LAZY),
+                          "recomputed_waves_pct": share(_native.ATTN_FLAG_RERUN),
                           "vs_certified": round(t / base, 3)})
-            kernels[f"attn_keybias_sharp_{tag}_x{int(scale)}_16h_274800x68700"] = entry
-            del qs, ks, vs, bs, flags
+            name = "lnscale" if scale == 8.0 else f"sharp_{tag}_x{int(scale)}"
+            kernels[f"attn_keybias_{name}{'_' + tag if scale == 8.0 else ''}_16h_274800x68700"] = entry
+            del qs, ks, vs, bs, flags, fl
         log("[bench] sharp-logit shapes done")
+
+    # The MFMA rate this part sustains on random data under its power limit:
+    # a plain hipBLASLt bf16 GEMM (torch.matmul, 16384^3, N(0,1) operands),
+    # and the same GEMM on all-zero operands (the multipliers do not toggle,
+    # so the clock stays high).  Context for the attention's fraction of the
+    # nominal peak; not part of the step.
+    ceiling = {}
+    n = 16_384
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    for tag in ("randn", "zeros"):
+        if tag == "zeros":
+            a = torch.zeros(n, n, device=dev, dtype=torch.bfloat16)
+            b = torch.zeros(n, n, device=dev, dtype=torch.bfloat16)
+        else:
+            a = torch.randn(n, n, generator=g, device=dev).bfloat16()
+            b = torch.randn(n, n, generator=g, device=dev).bfloat16()
+        fn = lambda: a @ b  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 7))
+        ceiling[f"hipblaslt_gemm_bf16_{n}_{tag}"] = kernel_entry(2.0 * n ** 3, t)
+        del a, b
+    torch.cuda.empty_cache()
+    gemm_tf = ceiling[f"hipblaslt_gemm_bf16_{n}_randn"]["tflops"]
+    log(f"[bench] hipBLASLt GEMM ceiling {gemm_tf:.0f} TFLOP/s on random data")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12
     traffic = None
@@ -479,7 +520,8 @@ def main(argv=None) -> int:
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": traffic, "kernel": "attn_main_kernel",
-                "flops_per_launch": f_attn}
+                "flops_per_launch": f_attn,
+                "gemm_ceiling_tflops": gemm_tf, "frac_of_gemm_ceiling": round(achieved / gemm_tf, 4)}
 
     e2e = None
     if not args.no_e2e:
@@ -512,6 +554,7 @@ def main(argv=None) -> int:
                                 "x 274800 queries x 68700 merged keys x d64 (200 frames x 1374 tokens)"),
                    "sm_scale": SM_SCALE, "bias": "log(count), bf16, [1,16,1,N]"},
         "kernels": kernels,
+        "mfma_ceiling": ceiling,
         "e2e": e2e,
         "roofline": roofline,
         "cpu_baseline": cpu,

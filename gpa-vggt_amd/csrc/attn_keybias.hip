@@ -18,9 +18,9 @@
 //     waves per SIMD).  Each K or V fragment read from LDS serves both of a
 //     wave's blocks.
 //   * One pass (attn_main_kernel), software-pipelined by one tile.  Every
-//     wave runs with a fixed softmax offset certified on tile 0; a wave that
-//     cannot certify it continues in place with a lazily moved offset (see
-//     there), so no work is discarded or recomputed.
+//     wave runs with a fixed softmax offset certified on tile 0, or taken
+//     from tile 0 and verified after the loop; a wave that can do neither
+//     runs with a lazily moved offset (see there).
 //   * K, V and the tile records stream through an LDS ring of 32-key tiles
 //     filled by buffer_load ... lds (DMA into LDS, no staging registers)
 //     several tiles ahead of the one being computed; keeping three tiles in
@@ -93,6 +93,20 @@ constexpr float kMInit = -1.0e30f;            // finite initial offset (all -inf
 // offset keeps the largest P in [1, 2^kUp].
 template <bool F16> constexpr float kUp = F16 ? 15.0f : 64.0f;
 template <bool F16> constexpr float kDown = F16 ? 1.0f : 96.0f;
+// A wave whose rows the bound cannot certify may instead take the fixed
+// offset m = x0 + kDown from tile 0 alone (its largest P is then >= 2^-kDown
+// whatever the later tiles hold) and have it verified after the loop: only
+// an overflow can go wrong, i.e. a later score more than kDown + ~100 (bf16;
+// P is finite below 2^128 and sums of up to 2^24 keys stay finite) or
+// kDown + 15.99 (fp16, P below 65504) log2 units above x0.  It does so when
+// every row's tile-0 scores span at most kOptRange log2 units (for Gaussian
+// scores the max over ~2^16 keys then sits about 0.55 times the largest
+// span of the wave's rows above x0: ~143 against the ~192 bf16 allows, ~11
+// against fp16's 16.99) and no key stands out: |q| (max_t c|k|_t -
+// mean_t c|k|_t) + (max_t c b_t - mean_t c b_t) <= kOptOutlier over the
+// per-tile maxima.  Other waves run the lazily moved offset from the start.
+template <bool F16> constexpr float kOptRange = F16 ? 20.0f : 260.0f;
+template <bool F16> constexpr float kOptOutlier = F16 ? 8.0f : 96.0f;
 constexpr int kRec = 36;                      // words per tile record
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -101,7 +115,7 @@ struct AttnArgs {
   const uint16_t* k;
   const uint16_t* v;
   const float* recs;      // [B*H][ntiles][kRec] tile records
-  const float* bounds;    // [B*H][2] maxima of the records' words 32 and 33
+  const float* bounds;    // [B*H][kBoundWords] row bounds (row_bounds_kernel)
   uint8_t* flags;         // [B*H][gx][kWaves] per wave: 1 = the lazily moved offset ran
   uint16_t* o;
   float* lse;
@@ -256,30 +270,43 @@ __global__ __launch_bounds__(256) void tile_records_kernel(RecArgs a) {
 }
 
 // Per (batch, head): the maxima over its tiles of c*max|k| and
-// c*max bias/sm_scale, so c*(|q| K + B) bounds every score of a query.
+// c*max bias/sm_scale, so c*(|q| K + B) bounds every score of a query, and
+// the means over its tiles of the same two words (how far the largest key
+// norm and the largest bias stand out from the rest of the keys).
+// kBoundWords floats per (batch, head).
+constexpr int kBoundWords = 4;
 __global__ __launch_bounds__(256) void row_bounds_kernel(const float* recs, float* bounds,
                                                          int64_t ntiles) {
-  __shared__ float part[2][4];
+  __shared__ float part[4][4];
   const float* r = recs + (int64_t)blockIdx.x * ntiles * kRec;
-  float kb = 0.f, bb = -INFINITY;
+  float kb = 0.f, bb = -INFINITY, ks = 0.f, bs = 0.f;
   for (int64_t t = threadIdx.x; t < ntiles; t += 256) {
-    kb = fmaxf(kb, r[t * kRec + kKT]);
-    bb = fmaxf(bb, r[t * kRec + kKT + 1]);
+    const float kt = r[t * kRec + kKT], bt = r[t * kRec + kKT + 1];
+    kb = fmaxf(kb, kt);
+    bb = fmaxf(bb, bt);
+    ks += kt;
+    bs += bt;
   }
 #pragma unroll
   for (int w = 1; w < 64; w <<= 1) {
     kb = fmaxf(kb, __shfl_xor(kb, w));
     bb = fmaxf(bb, __shfl_xor(bb, w));
+    ks += __shfl_xor(ks, w);
+    bs += __shfl_xor(bs, w);
   }
   if ((threadIdx.x & 63) == 0) {
     part[0][threadIdx.x >> 6] = kb;
     part[1][threadIdx.x >> 6] = bb;
+    part[2][threadIdx.x >> 6] = ks;
+    part[3][threadIdx.x >> 6] = bs;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    bounds[2 * blockIdx.x] = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
-    bounds[2 * blockIdx.x + 1] =
-        fmaxf(fmaxf(part[1][0], part[1][1]), fmaxf(part[1][2], part[1][3]));
+    float* out = bounds + (int64_t)kBoundWords * blockIdx.x;
+    out[0] = fmaxf(fmaxf(part[0][0], part[0][1]), fmaxf(part[0][2], part[0][3]));
+    out[1] = fmaxf(fmaxf(part[1][0], part[1][1]), fmaxf(part[1][2], part[1][3]));
+    out[2] = ((part[2][0] + part[2][1]) + (part[2][2] + part[2][3])) / (float)ntiles;
+    out[3] = ((part[3][0] + part[3][1]) + (part[3][2] + part[3][3])) / (float)ntiles;
   }
 }
 
@@ -314,14 +341,22 @@ __device__ __forceinline__ void tile_barrier() {
 // x0 >= m - kDown, i.e. the row's largest P is at least 2^-kDown.  A
 // certified wave runs the loop with no max, rescale or branch at all.  A wave
 // that cannot certify (B far above the row's real scores: sharp logits, or
-// fp16's narrow window) runs a second loop with a lazily moved offset
-// instead: m starts at x0 and, per tile, S(t), its exact row max, a
-// wave-uniform branch that rescales O and the row sums only where that max
-// exceeds m + kUp, then P(t) and its P.V product.  That loop is not
-// pipelined (S(t) and P(t) in the same iteration), so it holds fewer live
-// registers than the certified loop and leaves its register allocation and
-// schedule as they are.  Both loops issue the same DMAs, waits and barriers.
-// The per-wave flag records which loop ran (1 = lazy offset).
+// fp16's narrow window, which LayerNorm-scaled q and k already exceed) runs
+// the same loop with the tile-0 offset m = x0 + kDown when its tile-0 scores
+// are narrow and no key stands out (kOptRange, kOptOutlier): its largest P
+// is then >= 2^-kDown, and after the loop the row sums and O are checked for
+// an overflow (a later score more than ~192 / 17 log2 units above x0).  If a
+// wave of the workgroup overflowed, the workgroup streams the keys again and
+// every live wave recomputes its rows with the lazily moved offset.  Waves
+// outside both cases run that lazy loop from the start: m starts at x0 and,
+// per tile, S(t), its exact row max, a wave-uniform branch that rescales O
+// and the row sums only where that max exceeds m + kUp, then P(t) and its
+// P.V product.  That loop is not pipelined (S(t) and P(t) in the same
+// iteration), so it holds fewer live registers than the certified loop and
+// leaves its register allocation and schedule as they are (compared opcode
+// by opcode).  All loops issue the same DMAs, waits and barriers.  The
+// per-wave flag records what ran: bit 0 the output came from the lazy loop,
+// bit 1 the wave took the tile-0 offset, bit 2 the workgroup streamed twice.
 //
 // Five ring slots keep tile t (V), tile t+1 (K, bias) and the three tiles
 // in flight; the DMA of tile t+4 refills the slot of tile t-1.  Every wave
@@ -346,6 +381,7 @@ template <bool F16>
 __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   __shared__ MainTile ring0, ring1, ring2, ring3, ring4;
   __shared__ float rec_sink[64];
+  __shared__ uint32_t wg_fail[kWaves];   // per wave: its tile-0 offset overflowed
   MainTile* const ring[kMainSlots] = {&ring0, &ring1, &ring2, &ring3, &ring4};
 
   const int tid = threadIdx.x;
@@ -433,7 +469,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   float m_off[kBlk];
   f32x4 l_acc[kBlk];
   f32x16 o_acc[kBlk][2];
-  const float row_k = p.bounds[2 * bh], row_b = p.bounds[2 * bh + 1];
+  const float* const rb = p.bounds + (int64_t)kBoundWords * bh;
+  const float row_k = rb[0], row_b = rb[1], row_kmean = rb[2], row_bmean = rb[3];
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
     l_acc[j] = f32x4{};
@@ -544,30 +581,40 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   // SIMD gets the matrix pipe to itself.  Wave-uniform branch, taken before
   // the live path starts.
   if ((int64_t)qb * kQPerWG + wave * kQPerWave >= p.M) {
+    auto stream_only = [&]() {
 #pragma unroll
-    for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
-    wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
-    tile_barrier();
-    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
-    tile_barrier();
-    auto carry = [&](const int t, MainTile& Tissue) {
-      issue(t + kMainAhead, Tissue);
+      for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+      wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
+      tile_barrier();
       wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
       tile_barrier();
-    };
-    int t = 0;
-    for (; t + kMainSlots <= ntiles; t += kMainSlots) {
+      auto carry = [&](const int t, MainTile& Tissue) {
+        issue(t + kMainAhead, Tissue);
+        wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+        tile_barrier();
+      };
+      int t = 0;
+      for (; t + kMainSlots <= ntiles; t += kMainSlots) {
 #pragma unroll
-      for (int u = 0; u < kMainSlots; ++u) carry(t + u, *ring[(u + kMainAhead) % kMainSlots]);
-    }
-#pragma unroll
-    for (int u = 0; u < kMainSlots - 1; ++u)
-      if (t < ntiles) {
-        carry(t, *ring[(u + kMainAhead) % kMainSlots]);
-        ++t;
+        for (int u = 0; u < kMainSlots; ++u) carry(t + u, *ring[(u + kMainAhead) % kMainSlots]);
       }
-    if (lane == 0) flag_row[wave] = 0;
-    wait_vm<0>();
+#pragma unroll
+      for (int u = 0; u < kMainSlots - 1; ++u)
+        if (t < ntiles) {
+          carry(t, *ring[(u + kMainAhead) % kMainSlots]);
+          ++t;
+        }
+      wait_vm<0>();
+    };
+    stream_only();
+    // The workgroup's verdict on the tile-0 offsets (see the live path):
+    // if any wave overflowed, every wave streams the keys a second time.
+    if (lane == 0) wg_fail[wave] = 0;
+    tile_barrier();
+    const bool rerun = __builtin_amdgcn_readfirstlane(wg_fail[0] | wg_fail[1] | wg_fail[2] |
+                                                      wg_fail[3]) != 0;
+    if (rerun) stream_only();
+    if (lane == 0) flag_row[wave] = rerun ? 4 : 0;
     return;
   }
 
@@ -592,16 +639,35 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   tile_barrier();
   scores(*ring[0], s_cur);
   bool bad = false;
+  float x0s[kBlk];
 #pragma unroll
   for (int j = 0; j < kBlk; ++j) {
-    const float x0 = row_max(s_cur[j]);
-    m_off[j] = fmaxf(__builtin_fmaf(q_norm[j], row_k, row_b) - kUp<F16>, x0);
-    bad = bad || !(x0 >= m_off[j] - kDown<F16>);     // NaN scores fail too
+    x0s[j] = row_max(s_cur[j]);
+    m_off[j] = fmaxf(__builtin_fmaf(q_norm[j], row_k, row_b) - kUp<F16>, x0s[j]);
+    bad = bad || !(x0s[j] >= m_off[j] - kDown<F16>);     // NaN scores fail too
   }
   const bool fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+  bool opt = false;
   if (!fixed) {
+    // The tile-0 offset, taken where tile 0's scores are narrow and no key
+    // stands out (so that an overflow is unlikely); verified after the loop.
+    bool wide = false;
 #pragma unroll
-    for (int j = 0; j < kBlk; ++j) m_off[j] = kMInit;   // the first tile moves it
+    for (int j = 0; j < kBlk; ++j) {
+      float lo = INFINITY;                                 // min over the row's live scores
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lo = s_cur[j][r] > -INFINITY ? fminf(lo, s_cur[j][r]) : lo;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(lo),
+                                                       false, false);
+      lo = fminf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+      const float outl = __builtin_fmaf(q_norm[j], row_k - row_kmean, row_b - row_bmean);
+      wide = wide || !(x0s[j] > -INFINITY && x0s[j] < INFINITY) ||
+             !(x0s[j] - lo <= kOptRange<F16>) || !(outl <= kOptOutlier<F16>);
+    }
+    opt = __builtin_amdgcn_ballot_w64(wide) == 0;
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j)
+      m_off[j] = opt ? x0s[j] + kDown<F16> : kMInit;      // lazy: the first tile moves it
   }
   wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
   tile_barrier();
@@ -680,13 +746,58 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
         ++t;
       }
   };
-  if (fixed)
+  if (fixed || opt)
     run(std::false_type{});
   else
     run(std::true_type{});
-  if (lane == 0) flag_row[wave] = fixed ? 0 : 1;
-  // Drain the DMAs still in flight before the workgroup can exit.
+  // Drain the DMAs still in flight (before the ring is reused or the
+  // workgroup exits).
   wait_vm<0>();
+
+  // Verification of the tile-0 offset: any P that overflowed made its row
+  // sum infinite, a product that overflowed made O infinite (NaN counts as
+  // a failure too).  If a wave failed, the whole workgroup streams the keys
+  // again and every live wave recomputes its rows with the lazily moved
+  // offset (the ring is shared, so the others carry their share of the
+  // DMAs); the first results are discarded.
+  bool fail = false;
+  if (opt) {
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      fail = fail || !(sum_halves(l_acc[j][0]) < INFINITY);
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) fail = fail || !(fabsf(o_acc[j][db][r]) < INFINITY);
+    }
+  }
+  const bool fail_w = __builtin_amdgcn_ballot_w64(fail) != 0;   // every lane's verdict
+  if (lane == 0) wg_fail[wave] = fail_w ? 1u : 0u;
+  tile_barrier();
+  const bool rerun = __builtin_amdgcn_readfirstlane(wg_fail[0] | wg_fail[1] | wg_fail[2] |
+                                                    wg_fail[3]) != 0;
+  if (rerun) {
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      l_acc[j] = f32x4{};
+      o_acc[j][0] = f32x16{};
+      o_acc[j][1] = f32x16{};
+      m_off[j] = kMInit;
+    }
+#pragma unroll
+    for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+    wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
+    tile_barrier();
+    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    tile_barrier();
+    run(std::true_type{});
+    wait_vm<0>();
+    tile_barrier();
+  }
+  // Flag bits: 1 = the output comes from the lazily moved offset, 2 = the
+  // wave took the tile-0 offset, 4 = its workgroup streamed the keys twice.
+  if (lane == 0)
+    flag_row[wave] = (uint8_t)((rerun || !(fixed || opt) ? 1 : 0) | (opt ? 2 : 0) | (rerun ? 4 : 0));
 
   // O goes through LDS so that every store writes whole 128-byte rows:
   // eight rows of 16 bytes per lane per instruction instead of 8 bytes in
@@ -696,8 +807,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   // r / 32, query row r % 32) keeps its 16-byte chunk c at chunk c ^ (r & 7):
   // the writes of one instruction meet at most two to a bank, the row reads
   // not at all.  A wave's LDS operations run in order, so the reads need no
-  // further barrier.
-  tile_barrier();
+  // further barrier.  (The verdict barrier above, or the one after the
+  // second pass, already saw every wave's last ring read.)
   MainTile& slot_w = wave == 0 ? ring0 : wave == 1 ? ring1 : wave == 2 ? ring2 : ring3;
   uint16_t* const stage = reinterpret_cast<uint16_t*>(&slot_w);
 #pragma unroll
@@ -751,13 +862,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   }
 }
 
-// Workspace: one row of ntiles tile records per (batch, head), then two
-// floats of row bounds per (batch, head).
+// Workspace: one row of ntiles tile records per (batch, head), then
+// kBoundWords floats of row bounds per (batch, head), then one flag byte per
+// wave.
 size_t rec_bytes(int64_t B, int64_t H, int64_t N) {
   const int64_t ntiles = (N + kKT - 1) / kKT;
   return (size_t)(B * H * ntiles) * kRec * sizeof(float);
 }
-size_t bounds_bytes(int64_t B, int64_t H) { return (size_t)(B * H) * 2 * sizeof(float); }
+size_t bounds_bytes(int64_t B, int64_t H) { return (size_t)(B * H) * kBoundWords * sizeof(float); }
 size_t attn_ws_bytes(int64_t B, int64_t H, int64_t M, int64_t N) {
   const int64_t gx = (M + kQPerWG - 1) / kQPerWG;
   return rec_bytes(B, H, N) + bounds_bytes(B, H) + (size_t)(B * H * gx) * kWaves;

@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -283,10 +283,15 @@ def _sim_argmax_fake(a, b):
 # --------------------------------------------------------------------------
 
 # Workspace layout of the attention (gpa_attn_keybias_workspace_bytes): per
-# (batch, head) one 144-byte record per 32-key tile, then 8 bytes of row
+# (batch, head) one 144-byte record per 32-key tile, then 16 bytes of row
 # bounds per (batch, head), then one flag byte per 64-query wave (4 waves per
 # 256-query workgroup).
 _ATTN_TILE_KEYS, _ATTN_REC_BYTES, _ATTN_WG_QUERIES, _ATTN_WAVES = 32, 144, 256, 4
+_ATTN_BOUND_BYTES = 16
+# Bits of a wave's flag: its output comes from the lazily moved offset; it
+# took the fixed offset from tile 0 (verified after the loop); its workgroup
+# streamed the keys twice (a tile-0 offset of the workgroup overflowed).
+ATTN_FLAG_LAZY, ATTN_FLAG_TILE0, ATTN_FLAG_RERUN = 1, 2, 4
 
 
 def _attn_run(q, k, v, bias, sm_scale, return_lse):
@@ -369,9 +374,13 @@ def attn_keybias_offset_flags(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               return_lse: bool = False):
     """The attention plus which softmax offset each wave used (diagnostic).
 
-    Returns (o, lse, flags) with flags [B*H, ceil(M/256), 4] uint8: 1 where
-    the wave of 64 queries could not certify the fixed offset and ran the
-    lazily moved one, 0 where it kept the fixed offset (or holds no query).
+    Returns (o, lse, flags) with flags [B*H, ceil(M/256), 4] uint8, one per
+    wave of 64 queries: 0 where the score bound certified the fixed offset
+    (or the wave holds no query), otherwise the bits ATTN_FLAG_LAZY (the
+    output comes from the lazily moved offset), ATTN_FLAG_TILE0 (the wave
+    took the fixed offset from tile 0, verified after the loop) and
+    ATTN_FLAG_RERUN (a tile-0 offset of its workgroup overflowed, so the
+    workgroup streamed the keys again and recomputed with the lazy offset).
     """
     o, lse, ws = _attn_run(q, k, v, bias, sm_scale, return_lse)
     B, H, M, _ = q.shape
@@ -380,7 +389,7 @@ def attn_keybias_offset_flags(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return o, lse, torch.zeros(0, 0, _ATTN_WAVES, dtype=torch.uint8)
     ntiles = -(-N // _ATTN_TILE_KEYS)
     gx = -(-M // _ATTN_WG_QUERIES)
-    start = B * H * ntiles * _ATTN_REC_BYTES + B * H * 8
+    start = B * H * ntiles * _ATTN_REC_BYTES + B * H * _ATTN_BOUND_BYTES
     flags = ws[start:start + B * H * gx * _ATTN_WAVES].view(B * H, gx, _ATTN_WAVES)
     return o, lse, flags
 

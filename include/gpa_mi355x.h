@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 13
+#define GPA_ABI_VERSION 14
 
 enum {
   GPA_OK = 0,
@@ -116,8 +116,8 @@ int gpa_sim_argmax_f16(const void* a, const void* b,
 /* Bytes of device workspace gpa_attn_keybias_bf16 needs: per (batch, head)
  * one 144-byte record per 32-key tile, holding the keys' bias/sm_scale
  * (padded past N) and two per-tile maxima the kernel bounds its scores with,
- * 8 bytes of row maxima, and one flag byte per 32 queries.  The reference
- * wrapper allocates the analogous padded bias buffer
+ * 16 bytes of row maxima and means, and one flag byte per 64 queries.  The
+ * reference wrapper allocates the analogous padded bias buffer
  * (merging/fused_attention.py:159-160). */
 size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t N);
 

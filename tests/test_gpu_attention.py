@@ -102,10 +102,13 @@ def test_increasing_logits_force_rescales(dev):
 @pytest.mark.parametrize("lse", [False, True])
 def test_fixed_and_lazy_offset_waves_mix(dev, lse):
     """Rows whose score bound |q| max|k| sits far above their scores (more
-    than the 160 log2 units the fixed offset covers) make their wave run the
-    lazily moved offset; the other waves of the same workgroups keep the
-    fixed one.  Both must match the reference, and the flags say which wave
-    ran which."""
+    than the 160 log2 units the bound-certified offset covers) cannot keep
+    that offset.  Each boosted row points along key 40, ~230 log2 units above
+    its tile-0 scores: its wave either runs the lazily moved offset or takes
+    the tile-0 offset, overflows and has its workgroup recompute with the
+    lazy one.  Either way the boosted waves' outputs come from the lazy loop;
+    the other waves keep the certified offset (or were recomputed with their
+    workgroup), and everything matches the reference."""
     g = torch.Generator().manual_seed(11)
     M, N = 600, 1000
     q = torch.randn(1, 2, M, 64, generator=g) * 0.3
@@ -124,11 +127,17 @@ def test_fixed_and_lazy_offset_waves_mix(dev, lse):
     _check(o, ref)
     if lse:
         assert (l.cpu() - ref_lse).abs().max().item() < LSE_TOL
-    want = torch.zeros(2, 3, 4, dtype=torch.uint8)
-    want[:, 0, 0] = 1                                 # rows 5, 32-63
-    want[:, 1, 0] = 1                                 # row 300 (256 + 44)
-    want[:, 2, 0] = 1                                 # row 555 (512 + 43)
-    assert torch.equal(flags.cpu(), want)
+    f = flags.cpu()
+    boosted = torch.zeros(2, 3, 4, dtype=torch.bool)
+    boosted[:, :, 0] = True                           # rows 5, 32-63 / 300 / 555: wave 0 of each
+    assert ((f[boosted] & _native.ATTN_FLAG_LAZY) != 0).all()
+    rerun = (f & _native.ATTN_FLAG_RERUN) != 0        # per wave; uniform over a workgroup
+    assert torch.equal(rerun, rerun[:, :, :1].expand_as(rerun))
+    live = (torch.arange(12).view(1, 3, 4) * 64 < M).expand(2, 3, 4)   # waves holding queries
+    others = ~boosted & live
+    assert (f[others & ~rerun] == 0).all()
+    assert ((f[others & rerun] & _native.ATTN_FLAG_LAZY) != 0).all()
+    assert (f[~live] == (f[~live] & _native.ATTN_FLAG_RERUN)).all()   # no queries: 0 or 4
     # the same call through the op agrees bit for bit
     o2 = attention_keybias(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.125)
     assert torch.equal(o2, o)
@@ -304,3 +313,82 @@ def test_full_size_sharp_logits_mix_offsets(dev):
     print(f"[attn c3 sharp] sample max-abs {err.max().item():.3e} mean-abs "
           f"{err.mean().item():.3e}", flush=True)
     assert err.max().item() <= MAX_ABS and err.mean().item() <= 2e-3
+
+
+def _aligned_inputs(M, N, X, planted, seed, dtype):
+    """q and k of norm R = sqrt(X / (sm_scale log2 e)) in random directions, so
+    every score lies within X log2 units of 0, except tile 0's keys, of norm
+    R/4: tile 0's scores span ~X/6 and sit near 0, so every row takes the
+    tile-0 offset.  For each (row, key) in `planted` the key points along the
+    row's query, which puts that score at X log2 units, ~0.93 X above the
+    row's tile-0 max; the other rows' maxima stay within ~0.5 X of it."""
+    g = torch.Generator().manual_seed(seed)
+    R = math.sqrt(X / (0.125 / math.log(2.0)))
+    q = torch.randn(1, 2, M, 64, generator=g)
+    k = torch.randn(1, 2, N, 64, generator=g)
+    for row, key in planted:
+        k[:, :, key] = q[:, :, row]
+    q = q / q.norm(dim=-1, keepdim=True) * R
+    k = k / k.norm(dim=-1, keepdim=True) * R
+    k[:, :, :32] *= 0.25
+    v = torch.randn(1, 2, N, 64, generator=g)
+    return q.to(dtype).float(), k.to(dtype).float(), v.to(dtype).float()
+
+
+@pytest.mark.parametrize("dtype,X", [(torch.bfloat16, 300.0), (torch.float16, 26.0)])
+def test_tile0_offset_overflow_recomputes_workgroup(dev, dtype, X):
+    """Scores the bound cannot certify, with narrow tile-0 spans and no key
+    norm standing out: every wave takes the tile-0 offset.  Rows 10 and 300
+    meet a key aligned with their query in tile 7 (~0.93 X above x0: past
+    the ~224 (bf16: P = inf) / 17 (fp16) log2 units the tile-0 offset
+    survives), so their P overflows, and workgroups 0 and 1 stream the keys a
+    second time with the lazily moved offset; workgroup 2 keeps its verified
+    tile-0 offsets.  Outputs and LSE match the reference in all three."""
+    M, N = 600, 1000
+    planted = [(10, 7 * 32 + 5), (300, 7 * 32 + 20)]
+    q, k, v = _aligned_inputs(M, N, X, planted, seed=31, dtype=dtype)
+    args = [t.to(dev, dtype) for t in (q, k, v)]
+    o, l, flags = _native.attn_keybias_offset_flags(*args, None, 0.125, True)
+    ref, ref_lse = attention_reference(q, k, v, None, 0.125)
+    err = (o.float().cpu() - ref).abs()
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    lse_tol = LSE_TOL if dtype == torch.bfloat16 else 2.0 ** -10 / math.log(2.0) + 1e-5
+    assert (l.cpu() - ref_lse).abs().max().item() < lse_tol
+    f = flags.cpu()
+    T0, LZ, RR = _native.ATTN_FLAG_TILE0, _native.ATTN_FLAG_LAZY, _native.ATTN_FLAG_RERUN
+    assert (f[:, 0, 0] == T0 | LZ | RR).all() and (f[:, 1, 0] == T0 | LZ | RR).all()
+    assert ((f[:, :2] & (LZ | RR)) == LZ | RR).all()       # the whole workgroups recomputed
+    assert (f[:, 2, :2] == T0).all()                       # rows 512-599: verified tile-0 offset
+    assert (f[:, 2, 2:] == 0).all()                        # waves past M
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tile0_offset_layernorm_scale(dev, dtype):
+    """q and k at LayerNorm scale (features of variance 1.2^2, as the model's
+    qk norm with a gain of 1.2 leaves them) with the log-count bias: in fp16
+    the score bound sits
+    more than the 16 log2 units fp16's window certifies above most rows'
+    tile-0 max, so those waves take the verified tile-0 offset instead of the
+    lazily moved one; bf16 certifies them by the bound.  No wave recomputes,
+    and the outputs match the reference."""
+    g = torch.Generator().manual_seed(41)
+    M, N = 1024, 8192
+    q = (torch.randn(1, 2, M, 64, generator=g) * 1.2).to(dtype).float()
+    k = (torch.randn(1, 2, N, 64, generator=g) * 1.2).to(dtype).float()
+    v = (torch.randn(1, 2, N, 64, generator=g) / 8).to(dtype).float()
+    counts = torch.randint(1, 9, (1, 1, 1, N), generator=g).float()
+    b = counts.log().expand(1, 2, 1, N).to(dtype).float().contiguous()
+    o, l, flags = _native.attn_keybias_offset_flags(q.to(dev, dtype), k.to(dev, dtype),
+                                                    v.to(dev, dtype), b.to(dev, dtype), 0.125,
+                                                    True)
+    ref, ref_lse = attention_reference(q, k, v, b, 0.125)
+    err = (o.float().cpu() - ref).abs()
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    f = flags.cpu()
+    if dtype == torch.float16:
+        assert ((f == 0) | (f == _native.ATTN_FLAG_TILE0)).all()
+        assert (f == _native.ATTN_FLAG_TILE0).float().mean().item() > 0.5
+        assert (l.cpu() - ref_lse).abs().max().item() < 2.0 ** -10 / math.log(2.0) + 1e-5
+    else:
+        assert (f == 0).all()
+        assert (l.cpu() - ref_lse).abs().max().item() < LSE_TOL

@@ -140,12 +140,12 @@ def test_attn_noalloc_refuses_shapes_beyond_the_scratch():
 
 def test_attn_workspace_bytes():
     lib = _native.lib()
-    # per (batch, head): one 144-byte record per 32-key tile, 8 bytes of row
+    # per (batch, head): one 144-byte record per 32-key tile, 16 bytes of row
     # bounds, and one flag byte per wave (4 waves per 256 queries)
     assert lib.gpa_attn_keybias_workspace_bytes(1, 16, 274_800, 68_700) == \
-        16 * 2147 * 144 + 16 * 8 + 16 * 1074 * 4
-    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 256, 32) == 6 * 144 + 6 * 8 + 6 * 4
-    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 257, 33) == 6 * 2 * 144 + 6 * 8 + 6 * 8
+        16 * 2147 * 144 + 16 * 16 + 16 * 1074 * 4
+    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 256, 32) == 6 * 144 + 6 * 16 + 6 * 4
+    assert lib.gpa_attn_keybias_workspace_bytes(2, 3, 257, 33) == 6 * 2 * 144 + 6 * 16 + 6 * 8
     assert lib.gpa_attn_keybias_workspace_bytes(0, 3, 10, 33) == 0
 
 
