@@ -30,6 +30,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace gpa {
@@ -56,14 +57,45 @@ struct SimArgs {
   const uint16_t* b;
   float* out_max;      // final outputs (splits == 1)
   int64_t* out_idx;
-  float* part_max;     // [B][splits][M] partials (splits > 1)
-  int32_t* part_idx;
+  uint64_t* part;      // [B][M][splits] partial keys (splits > 1), see part_key
   int64_t M, N;
   int64_t a_sb, a_sm, b_sb, b_sn, omax_sb, oidx_sb;
   int splits;          // destination splits (1, 2, 4, 8 or a multiple of 8)
   int mblocks;         // source row blocks, padded to the mapping granularity
   int64_t n_chunk;     // destination rows per split (multiple of kTN)
+  // The last round's items, cut finer (D = 128, B = 1): the source blocks
+  // from tail_mb0 on give each of their splits to tail_sub workgroups of
+  // sub_chunk destination rows each, dispatched after the tail_item0 whole
+  // items, with partials [splits][tail_sub][tail_rows].  tail_sub = 0: none.
+  int tail_item0;
+  int tail_sub;
+  int tail_mb0;
+  int64_t tail_rows;
+  int64_t sub_chunk;
+  uint64_t* tail;
 };
+
+// A split's (max, index) as one 64-bit key whose unsigned order is the merge
+// order: a larger max wins, equal maxima go to the lower index (the split
+// order of the reference's strict `>`).  High word: the max's bits mapped to
+// unsigned order (-0 taken as +0, so the two compare equal); low word:
+// (0x7fffffff - idx) << 1, plus the sign of a zero max in bit 0, so the
+// value reported is the winning split's own.  Partials are never NaN (the
+// running max starts at -inf and NaN scores never win).
+__device__ __forceinline__ uint64_t part_key(float v, int idx) {
+  const uint32_t b = __float_as_uint(v);
+  const bool zero = (b & 0x7fffffffu) == 0;
+  const uint32_t c = zero ? 0u : b;
+  const uint32_t hi = (c & 0x80000000u) ? ~c : (c | 0x80000000u);
+  const uint32_t lo = ((0x7fffffffu - (uint32_t)idx) << 1) | (zero ? (b >> 31) : 0u);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ void key_part(uint64_t k, float& v, int& idx) {
+  const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+  const uint32_t c = (hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi;
+  v = __uint_as_float(c | ((lo & 1u) << 31));
+  idx = (int)(0x7fffffffu - (lo >> 1));
+}
 
 // Workgroup id -> (source block, split).  Workgroups are dispatched to the
 // eight XCDs round-robin, so `bid & 7` is the XCD; every XCD is given whole
@@ -84,6 +116,23 @@ __device__ __forceinline__ void map_block(const SimArgs& p, int bid, int& mblock
     split = x * k + (y % k);
     mblock = y / k;
   }
+}
+
+// Workgroup id -> (source block, split, sub-range): sub = -1 for a whole
+// split; the tail items keep the XCD of their split (bid & 7, as above).
+__device__ __forceinline__ void map_item(const SimArgs& p, int bid, int& mblock, int& split,
+                                         int& sub) {
+  if (p.tail_sub > 0 && bid >= p.tail_item0) {
+    const int t = bid - p.tail_item0, x = t & 7, y = t >> 3;
+    const int k = p.splits / 8;  // splits per XCD
+    sub = y % p.tail_sub;
+    const int rest = y / p.tail_sub;
+    split = x * k + rest % k;
+    mblock = p.tail_mb0 + rest / k;
+    return;
+  }
+  map_block(p, bid, mblock, split);
+  sub = -1;
 }
 
 template <int KS, bool F16>
@@ -254,9 +303,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
         p.out_max[batch * p.omax_sb + m] = bv;
         p.out_idx[batch * p.oidx_sb + m] = bi;
       } else {
-        const int64_t o = (batch * p.splits + split) * p.M + m;
-        p.part_max[o] = bv;
-        p.part_idx[o] = bi;
+        p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
       }
     }
   }
@@ -307,17 +354,20 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int quad = lane >> 4, l16 = lane & 15;
   const int64_t batch = blockIdx.y;
-  int mblock, split;
-  map_block(p, blockIdx.x, mblock, split);
+  int mblock, split, sub;
+  map_item(p, blockIdx.x, mblock, split, sub);
   // Uniform by construction; saying so keeps the DMA's buffer descriptor in
   // SGPRs (otherwise every issue runs a readfirstlane waterfall loop).
   mblock = __builtin_amdgcn_readfirstlane(mblock);
   split = __builtin_amdgcn_readfirstlane(split);
+  sub = __builtin_amdgcn_readfirstlane(sub);
   const int64_t m_wg = (int64_t)mblock * kRowsPerWG;
   if (m_wg >= p.M) return;
 
-  const int64_t n_begin = (int64_t)split * p.n_chunk;
-  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
+  const int64_t s_begin = (int64_t)split * p.n_chunk;
+  const int64_t n_begin = sub < 0 ? s_begin : s_begin + sub * p.sub_chunk;
+  const int64_t n_end = min(p.N, sub < 0 ? s_begin + p.n_chunk
+                                         : min(s_begin + p.n_chunk, n_begin + p.sub_chunk));
   const uint16_t* A = p.a + batch * p.a_sb;
   const uint16_t* Bm = p.b + batch * p.b_sb;
 
@@ -506,10 +556,11 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
       if (p.splits == 1) {
         p.out_max[batch * p.omax_sb + m] = bv;
         p.out_idx[batch * p.oidx_sb + m] = bi;
+      } else if (sub >= 0) {
+        const int64_t r = m - (int64_t)p.tail_mb0 * kRowsPerWG;
+        p.tail[(r * p.splits + split) * p.tail_sub + sub] = part_key(bv, bi);
       } else {
-        const int64_t o = (batch * p.splits + split) * p.M + m;
-        p.part_max[o] = bv;
-        p.part_idx[o] = bi;
+        p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
       }
     }
   }
@@ -726,31 +777,48 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
           p.out_max[batch * p.omax_sb + m] = bv;
           p.out_idx[batch * p.oidx_sb + m] = bi;
         } else {
-          const int64_t o = (batch * p.splits + split) * p.M + m;
-          p.part_max[o] = bv;
-          p.part_idx[o] = bi;
+          p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
         }
       }
     }
   }
 }
 
-// Merge per-split partials in split order; strict `>` keeps the earlier
-// split (lower destination indices) on ties.
+// Merge a row's partial keys: the largest key, i.e. the largest max and,
+// among equal maxima, the lowest index -- what the reference's strict `>`
+// across destination tiles keeps.  A row's keys are contiguous, so a wave
+// reads whole lines, 16 bytes per load, all before any compare (a
+// compare-then-load loop over [split][row] planes took 31 us for 75,000
+// rows x 16 splits, 8 % of that call).
 __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_t B) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= B * p.M) return;
   const int64_t batch = t / p.M, m = t % p.M;
-  const int64_t base = batch * p.splits * p.M + m;
-  float bv = p.part_max[base];
-  int bi = p.part_idx[base];
-  for (int s = 1; s < p.splits; ++s) {
-    const float v = p.part_max[base + s * p.M];
-    if (v > bv) {
-      bv = v;
-      bi = p.part_idx[base + s * p.M];
+  const int64_t r = m - (int64_t)p.tail_mb0 * rows_per_wg(4);
+  const bool in_tail = p.tail_sub > 0 && r >= 0;
+  const int parts = in_tail ? p.splits * p.tail_sub : p.splits;
+  const uint64_t* k = in_tail ? p.tail + r * parts : p.part + t * p.splits;
+  uint64_t best = 0;
+  constexpr int kBatch = 16;
+  for (int s0 = 0; s0 < parts; s0 += kBatch) {
+    uint64_t v[kBatch];
+    if (s0 + kBatch <= parts && parts % 2 == 0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; u += 2) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(k + s0 + u);
+        v[u] = ((uint64_t)w[1] << 32) | w[0];
+        v[u + 1] = ((uint64_t)w[3] << 32) | w[2];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = s0 + u < parts ? k[s0 + u] : 0;
     }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) best = v[u] > best ? v[u] : best;
   }
+  float bv;
+  int bi;
+  key_part(best, bv, bi);
   p.out_max[batch * p.omax_sb + m] = bv;
   p.out_idx[batch * p.oidx_sb + m] = bi;
 }
@@ -759,8 +827,31 @@ struct SimPlan {
   int splits;
   int mblocks;       // padded source blocks
   int64_t n_chunk;
+  int tail_sub;      // 0: no tail (see SimArgs)
+  int tail_mb0;
+  int64_t tail_rows;
+  int64_t sub_chunk;
+  size_t part_bytes;  // [B][M][splits] partial keys
   size_t ws_bytes;
 };
+
+// Workgroups the current device holds at two per CU (the similarity
+// kernels' occupancy): the round size the tail is cut for.
+int device_slots() {
+  static std::mutex mu;
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cache[dev] = 2 * cus;
+  }
+  return cache[dev];
+}
 
 // Largest feature dim of the GEMM-tiled kernel (D > 256).
 constexpr int64_t kMaxD = 4096;
@@ -790,7 +881,31 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   const int64_t per = (N + splits - 1) / splits;
   const int gran = gemm ? kGT : kTN;      // whole destination tiles per split
   pl.n_chunk = (per + gran - 1) / gran * gran;
-  pl.ws_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
+  pl.part_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
+  pl.ws_bytes = pl.part_bytes;
+  // The last round (D = 128, one batch, whole XCD-mapped splits): when the
+  // (block, split) items leave a partial last round of `rem` items, the last
+  // T = ceil(rem / splits) source blocks give each split to P workgroups of
+  // a P-th of its destination rows, P = slots / (T * splits), so the last
+  // round is one round of short items instead of a few long ones.
+  // (75,000 x 25,000, 16 splits: 4,688 items = 9 rounds of 512 + 80 items;
+  // the last 5 blocks' 80 (block, split) items become 480 of 288 rows.)
+  if (D == 128 && B == 1 && splits >= 8 && splits % 8 == 0) {
+    const int64_t slots = device_slots();
+    const int64_t items = mb * splits;
+    const int64_t rem = items % slots;
+    if (items > slots && rem != 0) {
+      const int64_t T = (rem + splits - 1) / splits;
+      const int64_t P = slots / (T * splits);
+      if (P >= 2 && T < mb) {
+        pl.tail_sub = (int)P;
+        pl.tail_mb0 = (int)(mb - T);
+        pl.tail_rows = M - (mb - T) * rows;
+        pl.sub_chunk = ((pl.n_chunk + P - 1) / P + 31) / 32 * 32;
+        pl.ws_bytes += (size_t)(splits * P * pl.tail_rows) * (sizeof(float) + sizeof(int32_t));
+      }
+    }
+  }
   return pl;
 }
 
@@ -876,16 +991,25 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
   p.splits = pl.splits;
   p.mblocks = pl.mblocks;
   p.n_chunk = pl.n_chunk;
+  p.tail_sub = pl.tail_sub;
+  p.tail_mb0 = pl.tail_mb0;
+  p.tail_rows = pl.tail_rows;
+  p.sub_chunk = pl.sub_chunk;
+  p.tail_item0 = pl.tail_mb0 * pl.splits;
   if (pl.splits > 1) {
     if (!workspace || workspace_bytes < pl.ws_bytes) {
       gpa_set_error("%s: workspace of %zu bytes required, %zu given", fn,
                     pl.ws_bytes, workspace ? workspace_bytes : (size_t)0);
       return GPA_E_WORKSPACE;
     }
-    p.part_max = (float*)workspace;
-    p.part_idx = (int32_t*)((char*)workspace + (size_t)(B * pl.splits * M) * sizeof(float));
+    p.part = (uint64_t*)workspace;
+    if (pl.tail_sub > 0) p.tail = (uint64_t*)((char*)workspace + pl.part_bytes);
   }
-  const int64_t grid_x = (int64_t)pl.mblocks * pl.splits;
+  // Whole (block, split) items, then the tail's sub-range items.
+  const int64_t grid_x =
+      pl.tail_sub > 0 ? (int64_t)pl.tail_mb0 * pl.splits +
+                            (int64_t)(pl.mblocks - pl.tail_mb0) * pl.splits * pl.tail_sub
+                      : (int64_t)pl.mblocks * pl.splits;
   if (grid_x > 0x7fffffff) {
     gpa_set_error("%s: grid too large", fn);
     return GPA_E_UNSUPPORTED;

@@ -211,3 +211,32 @@ def test_full_size_similarity_workload(dev):
     assert np.abs(vmax[0, rows.to(dev)].cpu().numpy() - fmax[0]).max() < 1e-5
     sure = fgap[0] > 1e-5
     assert np.array_equal(vidx[0, rows.to(dev)].cpu().numpy()[sure], fidx[0][sure])
+
+
+def test_last_round_cut_into_sub_ranges(dev):
+    """17,152 x 8,192 x 128: 67 source blocks x 16 destination splits = 1,072
+    workgroups, two rounds of 512 plus 48, so the last 3 blocks give each
+    split to 10 workgroups of a tenth of its rows (partials merged in
+    destination order).  Against the fp64 brute force; tail rows whose best
+    destination row is duplicated in other splits and sub-ranges resolve to
+    the first copy."""
+    M, N = 67 * 256, 8192
+    a = _unit_bf16_values((1, M, 128), seed=91)
+    b = _unit_bf16_values((1, N, 128), seed=92)
+    g = torch.Generator().manual_seed(93)
+    tail = torch.arange(64 * 256, M)
+    rows = tail[torch.randperm(tail.numel(), generator=g)[:32]]
+    copies = torch.randperm(N, generator=g)[:96].view(3, 32).sort(dim=0).values
+    base = _unit_bf16_values((1, 32, 128), seed=94)
+    for c in range(3):
+        b[0, copies[c]] = base[0]
+    a[0, rows] = base[0]
+    vmax, vidx = fused_similarity_argmax(a.to(dev), b.to(dev))
+    vmax, vidx = vmax.cpu().numpy(), vidx.cpu().numpy()
+    fmax, fidx, gap = sim_argmax_fp64(a, b)
+    assert np.abs(vmax - fmax).max() < 1e-5
+    sure = gap > 1e-5
+    assert sure.mean() > 0.9
+    assert np.array_equal(vidx[sure], fidx[sure])
+    assert np.array_equal(vidx[0, rows.numpy()], copies[0].numpy())
+    assert np.array_equal(fidx[0, rows.numpy()], copies[0].numpy())
