@@ -861,15 +861,14 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   const bool gemm = D > 256;
   const int rows = gemm ? kGT : rows_per_wg((int)(D / 32));
   const int64_t mb = (M + rows - 1) / rows;
-  // Split the destination range until the grid holds >= 4096 workgroups
-  // (16 per CU on 256 CUs, eight rounds at two per CU) or a split would drop
-  // below 512 rows.  Once there are several splits, use at least 8 so that
-  // each XCD owns one range.  (75,000 x 25,000: 16 splits of 1,600 rows ran
-  // 358 us against 393 us for 8 splits of 3,136 and 366 / 380 / 415 us for
-  // 24 / 32 / 48: the shorter workgroups even out the last round, and below
-  // ~1,000 rows the per-workgroup start-up costs more than that saves.)
+  // Split the destination range until the grid holds >= 2048 workgroups
+  // (8 per CU on 256 CUs) or a split would drop below 512 rows.  Once there
+  // are several splits, use at least 8 so that each XCD owns one range.
+  // (75,000 x 25,000 with the last round cut as below: 8 splits 350 us,
+  // 16 splits 366 us; 32 splits without a cut 397 us: below ~1,000 rows a
+  // workgroup's start-up costs more than its work.)
   int splits = 1;
-  while (splits < 16 && mb * B * splits < 4096 && N / (splits * 2) >= 512) splits *= 2;
+  while (splits < 16 && mb * B * splits < 2048 && N / (splits * 2) >= 512) splits *= 2;
   if (splits > 1 && splits < 8 && N / 8 >= 512) splits = 8;
   pl.splits = splits;
   int64_t mbp = mb;
@@ -886,17 +885,19 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   // The last round (D = 128, one batch, whole XCD-mapped splits): when the
   // (block, split) items leave a partial last round of `rem` items, the last
   // T = ceil(rem / splits) source blocks give each split to P workgroups of
-  // a P-th of its destination rows, P = slots / (T * splits), so the last
-  // round is one round of short items instead of a few long ones.
-  // (75,000 x 25,000, 16 splits: 4,688 items = 9 rounds of 512 + 80 items;
-  // the last 5 blocks' 80 (block, split) items become 480 of 288 rows.)
+  // a P-th of its destination rows, P = 2 slots / (T * splits), so the end
+  // of the call is up to two rounds of short items instead of a partial
+  // round of long ones.  (75,000 x 25,000: 2,344 items = 4 rounds of 512 +
+  // 296; the last 37 blocks' 296 items become 888 of 1,056 rows: 364 ->
+  // 350 us.  200 frames: 6,504 = 12 rounds + 360; the last 45 blocks' items
+  // halved: 2,453 -> 2,415 us.)
   if (D == 128 && B == 1 && splits >= 8 && splits % 8 == 0) {
     const int64_t slots = device_slots();
     const int64_t items = mb * splits;
     const int64_t rem = items % slots;
     if (items > slots && rem != 0) {
       const int64_t T = (rem + splits - 1) / splits;
-      const int64_t P = slots / (T * splits);
+      const int64_t P = 2 * slots / (T * splits);
       if (P >= 2 && T < mb) {
         pl.tail_sub = (int)P;
         pl.tail_mb0 = (int)(mb - T);

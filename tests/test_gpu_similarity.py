@@ -216,8 +216,8 @@ def test_full_size_similarity_workload(dev):
 def test_last_round_cut_into_sub_ranges(dev):
     """17,152 x 8,192 x 128: 67 source blocks x 16 destination splits = 1,072
     workgroups, two rounds of 512 plus 48, so the last 3 blocks give each
-    split to 10 workgroups of a tenth of its rows (partials merged in
-    destination order).  Against the fp64 brute force; tail rows whose best
+    split to 21 workgroups of 32 rows each, the last five of them empty
+    (partials merged in destination order).  Against the fp64 brute force; tail rows whose best
     destination row is duplicated in other splits and sub-ranges resolve to
     the first copy."""
     M, N = 67 * 256, 8192

@@ -81,12 +81,14 @@ def test_workspace_bytes():
     big = lib.gpa_sim_argmax_workspace_bytes(1, 75_000, 25_000, 128)
     assert big > 0 and big % 8 == 0
     assert big >= 75_000 * 8                          # one (max, idx) pair per row and split
-    # 75,000 x 25,000 on 256 CUs: 16 splits of 1,600 rows (293 x 16 = 9 rounds
-    # of 512 workgroups + 80), and the last 5 source blocks (1,272 rows) cut
-    # into 6 sub-ranges per split: 16 x 6 more (max, idx) pairs per tail row
-    assert big == 16 * 75_000 * 8 + 16 * 6 * 1_272 * 8
-    # 200 frames: 813 x 8 = 12 rounds + 360 items: too many for a second cut
-    assert lib.gpa_sim_argmax_workspace_bytes(1, 207_955, 66_845, 128) == 8 * 207_955 * 8
+    # 75,000 x 25,000 on 256 CUs: 8 splits of 3,136 rows (293 x 8 = 4 rounds
+    # of 512 workgroups + 296), and the last 37 source blocks (9,464 rows)
+    # cut into 3 sub-ranges per split: 8 x 3 more (max, idx) keys per tail row
+    assert big == 8 * 75_000 * 8 + 8 * 3 * 9_464 * 8
+    # 200 frames: 813 x 8 = 12 rounds + 360 items: the last 45 blocks (11,347
+    # rows) halved
+    assert lib.gpa_sim_argmax_workspace_bytes(1, 207_955, 66_845, 128) == \
+        8 * 207_955 * 8 + 8 * 2 * 11_347 * 8
 
 
 def _attn(**kw):
