@@ -126,6 +126,7 @@ struct AttnArgs {
   uint32_t k_bytes, v_bytes, rec_bytes;  // extent of one (batch, head) slice
   float c;                                // sm_scale * log2(e)
   int o16;                                // O rows 16-byte aligned (16-byte stores)
+  int no_bound;                           // records without key maxima: no score bound
 };
 
 struct RecArgs {
@@ -317,6 +318,24 @@ __global__ __launch_bounds__(256) void row_bounds_kernel(const float* recs, floa
 // lgkmcnt(0) retires this wave's LDS reads before any slot is refilled.
 __device__ __forceinline__ void tile_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Tile records of a call without bias, bf16 (the own-frame and frame
+// attentions): bias/sm_scale = 0 for the keys, -inf past N, and no key
+// maxima, so the kernel has no score bound and every wave takes the tile-0
+// offset or the lazily moved one.  Writing these costs nothing like reading
+// every key (tile_records_kernel reads all of K: 0.11 of the own-frame
+// call's 1.86 ms).  Also zeroes the row-bound words the kernel reads.
+__global__ __launch_bounds__(256) void fill_records_kernel(float* recs, float* bounds,
+                                                           int64_t ntiles, int64_t N,
+                                                           int64_t total, int64_t rows) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < total * kRec) {
+    const int64_t t = i / kRec, w = i - t * kRec;
+    const int64_t n = (t % ntiles) * kKT + w;
+    recs[i] = (w < kKT && n >= N) ? -INFINITY : 0.f;
+  }
+  if (i < rows * kBoundWords) bounds[i] = 0.f;
 }
 
 // The attention kernel: software-pipelined by one tile.
@@ -646,7 +665,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     m_off[j] = fmaxf(__builtin_fmaf(q_norm[j], row_k, row_b) - kUp<F16>, x0s[j]);
     bad = bad || !(x0s[j] >= m_off[j] - kDown<F16>);     // NaN scores fail too
   }
-  const bool fixed = __builtin_amdgcn_ballot_w64(bad) == 0;
+  // (Without the key maxima there is no bound to certify anything with.)
+  const bool fixed = !p.no_bound && __builtin_amdgcn_ballot_w64(bad) == 0;
   bool opt = false;
   if (!fixed) {
     // The tile-0 offset, taken where tile 0's scores are narrow and no key
@@ -982,7 +1002,13 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   ra.mul = 1.0f / sm_scale;
   ra.c = c;
   ra.total = B * H * ntiles;
-  {
+  float* bounds = (float*)((char*)workspace + rec_bytes(B, H, N));
+  const bool no_bound = bias_kind == GPA_BIAS_NONE && !F16;
+  if (no_bound) {
+    const int64_t n = ra.total * kRec;
+    hipLaunchKernelGGL(fill_records_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       (float*)workspace, bounds, ntiles, N, ra.total, B * H);
+  } else {
     const dim3 rgrid((unsigned)((ra.total + kRecTiles - 1) / kRecTiles)), rblock(256);
     switch (bias_kind) {
       case GPA_BIAS_F32:
@@ -1005,14 +1031,15 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
                   hipGetErrorString(e));
     return GPA_E_LAUNCH;
   }
-  float* bounds = (float*)((char*)workspace + rec_bytes(B, H, N));
-  hipLaunchKernelGGL(row_bounds_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s,
-                     (const float*)workspace, bounds, ntiles);
-  e = hipGetLastError();
-  if (e != hipSuccess) {
-    gpa_set_error("%s: row-bound pre-pass launch failed: %s", fn,
-                  hipGetErrorString(e));
-    return GPA_E_LAUNCH;
+  if (!no_bound) {
+    hipLaunchKernelGGL(row_bounds_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s,
+                       (const float*)workspace, bounds, ntiles);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      gpa_set_error("%s: row-bound pre-pass launch failed: %s", fn,
+                    hipGetErrorString(e));
+      return GPA_E_LAUNCH;
+    }
   }
 
   AttnArgs p{};
@@ -1037,6 +1064,7 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   p.rec_bytes = (uint32_t)(ntiles * kRec * sizeof(float));
   p.c = c;
   p.o16 = ((uintptr_t)o % 16 == 0 && o_sm % 8 == 0 && o_sb % 8 == 0 && o_sh % 8 == 0) ? 1 : 0;
+  p.no_bound = no_bound ? 1 : 0;
 
   const dim3 grid((unsigned)gx, (unsigned)(B * H)), block(kThreads);
   hipLaunchKernelGGL(attn_main_kernel<F16>, grid, block, 0, s, p);
