@@ -55,7 +55,8 @@ __device__ __forceinline__ void wait_vm() {
 struct SimArgs {
   const uint16_t* a;
   const uint16_t* b;
-  float* out_max;      // final outputs (splits == 1)
+  void* out_max;       // final outputs (splits == 1 or the merge): max_dtype elements
+  int max_dtype;
   int64_t* out_idx;
   uint64_t* part;      // [B][M][splits] partial keys (splits > 1), see part_key
   int64_t M, N;
@@ -95,6 +96,17 @@ __device__ __forceinline__ void key_part(uint64_t k, float& v, int& idx) {
   const uint32_t c = (hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi;
   v = __uint_as_float(c | ((lo & 1u) << 31));
   idx = (int)(0x7fffffffu - (lo >> 1));
+}
+
+// The row max in the caller's element type (fp32, or bf16 / fp16 rounded
+// to nearest even, as torch's cast does).
+__device__ __forceinline__ void store_max(const SimArgs& p, int64_t o, float v) {
+  if (p.max_dtype == GPA_DTYPE_BF16)
+    static_cast<__bf16*>(p.out_max)[o] = (__bf16)v;
+  else if (p.max_dtype == GPA_DTYPE_F16)
+    static_cast<_Float16*>(p.out_max)[o] = (_Float16)v;
+  else
+    static_cast<float*>(p.out_max)[o] = v;
 }
 
 // Workgroup id -> (source block, split).  Workgroups are dispatched to the
@@ -300,7 +312,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_kernel(SimArgs p) {
     const int64_t m = m_wg + wave * (kSB * 16) + sb * 16 + l16;
     if (quad == 0 && m < p.M) {
       if (p.splits == 1) {
-        p.out_max[batch * p.omax_sb + m] = bv;
+        store_max(p, batch * p.omax_sb + m, bv);
         p.out_idx[batch * p.oidx_sb + m] = bi;
       } else {
         p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
@@ -554,7 +566,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
     const int64_t m = m_wg + wave * (kSB * 16) + sb * 16 + l16;
     if (quad == 0 && m < p.M) {
       if (p.splits == 1) {
-        p.out_max[batch * p.omax_sb + m] = bv;
+        store_max(p, batch * p.omax_sb + m, bv);
         p.out_idx[batch * p.oidx_sb + m] = bi;
       } else if (sub >= 0) {
         const int64_t r = m - (int64_t)p.tail_mb0 * kRowsPerWG;
@@ -774,7 +786,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
       const int64_t m = m_wg + r;
       if (m < p.M) {
         if (p.splits == 1) {
-          p.out_max[batch * p.omax_sb + m] = bv;
+          store_max(p, batch * p.omax_sb + m, bv);
           p.out_idx[batch * p.oidx_sb + m] = bi;
         } else {
           p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
@@ -819,7 +831,7 @@ __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_
   float bv;
   int bi;
   key_part(best, bv, bi);
-  p.out_max[batch * p.omax_sb + m] = bv;
+  store_max(p, batch * p.omax_sb + m, bv);
   p.out_idx[batch * p.oidx_sb + m] = bi;
 }
 
@@ -925,7 +937,8 @@ namespace {
 // Shared by the bf16 and fp16 entry points: the kernels differ only in the
 // MFMA instruction; `fn` names the entry point in error messages.
 template <bool F16>
-int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max, int64_t* out_idx,
+int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, int max_dtype,
+                   int64_t* out_idx,
                    int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb, int64_t a_sm,
                    int64_t b_sb, int64_t b_sn, int64_t omax_sb, int64_t oidx_sb, void* workspace,
                    size_t workspace_bytes, void* stream) {
@@ -938,6 +951,10 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
   if (B == 0 || M == 0) return GPA_OK;
   if (N == 0) {
     gpa_set_error("%s: empty destination set (N=0)", fn);
+    return GPA_E_INVALID;
+  }
+  if (max_dtype != GPA_DTYPE_F32 && max_dtype != GPA_DTYPE_BF16 && max_dtype != GPA_DTYPE_F16) {
+    gpa_set_error("%s: unknown max_dtype %d", fn, max_dtype);
     return GPA_E_INVALID;
   }
   if (!a || !b || !out_max || !out_idx) {
@@ -980,6 +997,7 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
   p.a = (const uint16_t*)a;
   p.b = (const uint16_t*)b;
   p.out_max = out_max;
+  p.max_dtype = max_dtype;
   p.out_idx = out_idx;
   p.M = M;
   p.N = N;
@@ -1044,22 +1062,22 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, float* out_max,
 
 }  // namespace
 
-extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, float* out_max, int64_t* out_idx,
-                                   int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
+extern "C" int gpa_sim_argmax_bf16(const void* a, const void* b, void* out_max, int max_dtype,
+                                   int64_t* out_idx, int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
                                    int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
                                    int64_t oidx_sb, void* workspace, size_t workspace_bytes,
                                    void* stream) {
-  return sim_argmax_run<false>("gpa_sim_argmax_bf16", a, b, out_max, out_idx, B, M, N, D, a_sb,
-                               a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace, workspace_bytes,
-                               stream);
+  return sim_argmax_run<false>("gpa_sim_argmax_bf16", a, b, out_max, max_dtype, out_idx, B, M, N,
+                               D, a_sb, a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace,
+                               workspace_bytes, stream);
 }
 
-extern "C" int gpa_sim_argmax_f16(const void* a, const void* b, float* out_max, int64_t* out_idx,
-                                  int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
+extern "C" int gpa_sim_argmax_f16(const void* a, const void* b, void* out_max, int max_dtype,
+                                  int64_t* out_idx, int64_t B, int64_t M, int64_t N, int64_t D, int64_t a_sb,
                                   int64_t a_sm, int64_t b_sb, int64_t b_sn, int64_t omax_sb,
                                   int64_t oidx_sb, void* workspace, size_t workspace_bytes,
                                   void* stream) {
-  return sim_argmax_run<true>("gpa_sim_argmax_f16", a, b, out_max, out_idx, B, M, N, D, a_sb,
-                              a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace, workspace_bytes,
-                              stream);
+  return sim_argmax_run<true>("gpa_sim_argmax_f16", a, b, out_max, max_dtype, out_idx, B, M, N,
+                              D, a_sb, a_sm, b_sb, b_sn, omax_sb, oidx_sb, workspace,
+                              workspace_bytes, stream);
 }

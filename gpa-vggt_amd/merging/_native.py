@@ -33,7 +33,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgpa_mi355x.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 GPA_OK = 0
 GPA_E_INVALID = -1
@@ -53,6 +53,8 @@ NOALLOC_SCRATCH_BYTES = 32 << 20
 GPA_DTYPE_F32 = 0
 GPA_DTYPE_BF16 = 1
 GPA_DTYPE_F16 = 2
+_DTYPE_CODES = {torch.float32: GPA_DTYPE_F32, torch.bfloat16: GPA_DTYPE_BF16,
+                          torch.float16: GPA_DTYPE_F16}
 GPA_MERGE_SUM = 0
 GPA_MERGE_MEAN = 1
 
@@ -76,7 +78,7 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.gpa_sim_argmax_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.gpa_sim_argmax_bf16.restype = ctypes.c_int
     lib.gpa_sim_argmax_bf16.argtypes = [
-        _vp, _vp, _vp, _vp,            # a, b, out_max, out_idx
+        _vp, _vp, _vp, ctypes.c_int, _vp,  # a, b, out_max, max_dtype, out_idx
         _i64, _i64, _i64, _i64,        # B, M, N, D
         _i64, _i64, _i64, _i64,        # a_sb, a_sm, b_sb, b_sn
         _i64, _i64,                    # omax_sb, oidx_sb
@@ -239,9 +241,11 @@ def _rows_ok(t: torch.Tensor, align_elems: int) -> bool:
 # --------------------------------------------------------------------------
 
 @torch.library.custom_op("gpa::sim_argmax", mutates_args=())
-def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Row max (fp32) and lowest-index argmax (int64) of a @ b^T; a and b
-    both bf16 or both fp16."""
+def sim_argmax(a: torch.Tensor, b: torch.Tensor,
+               max_in_input_dtype: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Row max and lowest-index argmax (int64) of a @ b^T; a and b both bf16
+    or both fp16.  The max is fp32, or a's dtype (the fp32 max rounded to
+    nearest even, written by the kernel) with max_in_input_dtype."""
     dev = _require_gpu(a, b)
     if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError(f"gpa::sim_argmax takes two bf16 or two fp16 inputs, got "
@@ -254,7 +258,8 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Te
         b = b.contiguous()
     B, M, D = a.shape
     N = b.shape[1]
-    out_max = torch.empty(B, M, device=dev, dtype=torch.float32)
+    max_dtype = a.dtype if max_in_input_dtype else torch.float32
+    out_max = torch.empty(B, M, device=dev, dtype=max_dtype)
     out_idx = torch.empty(B, M, device=dev, dtype=torch.int64)
     if B == 0 or M == 0:
         return out_max, out_idx
@@ -264,7 +269,8 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Te
     with torch.cuda.device(dev):
         fn = L.gpa_sim_argmax_f16 if a.dtype == torch.float16 else L.gpa_sim_argmax_bf16
         rc = fn(
-            a.data_ptr(), b.data_ptr(), out_max.data_ptr(), out_idx.data_ptr(),
+            a.data_ptr(), b.data_ptr(), out_max.data_ptr(), _DTYPE_CODES[max_dtype],
+            out_idx.data_ptr(),
             B, M, N, D, _st(a, 0), _rs(a, 1), _st(b, 0), _rs(b, 1),
             _st(out_max, 0), _st(out_idx, 0),
             ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
@@ -273,9 +279,10 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor) -> Tuple[torch.Tensor, torch.Te
 
 
 @sim_argmax.register_fake
-def _sim_argmax_fake(a, b):
+def _sim_argmax_fake(a, b, max_in_input_dtype=False):
     B, M, _ = a.shape
-    return a.new_empty(B, M, dtype=torch.float32), a.new_empty(B, M, dtype=torch.int64)
+    return (a.new_empty(B, M, dtype=a.dtype if max_in_input_dtype else torch.float32),
+            a.new_empty(B, M, dtype=torch.int64))
 
 
 # --------------------------------------------------------------------------
@@ -402,8 +409,7 @@ def _attn_keybias_fake(q, k, v, bias, sm_scale, return_lse):
     return o, lse
 
 
-_MERGE_DTYPES = {torch.float32: GPA_DTYPE_F32, torch.bfloat16: GPA_DTYPE_BF16,
-                 torch.float16: GPA_DTYPE_F16}
+_MERGE_DTYPES = _DTYPE_CODES
 
 
 @torch.library.custom_op("gpa::merge_heads", mutates_args=())

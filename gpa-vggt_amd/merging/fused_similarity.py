@@ -52,5 +52,7 @@ def fused_similarity_argmax(a: torch.Tensor, b: torch.Tensor):
         pad = 32 - D % 32
         a = F.pad(a, (0, pad))
         b = F.pad(b, (0, pad))
-    node_max, node_idx = torch.ops.gpa.sim_argmax(a, b)
+    # The kernel writes the max in a's 16-bit dtype itself when that is the
+    # output dtype (fp32 inputs keep the fp32 max).
+    node_max, node_idx = torch.ops.gpa.sim_argmax(a, b, out_dtype == a.dtype)
     return node_max.to(out_dtype), node_idx

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GPA_ABI_VERSION 14
+#define GPA_ABI_VERSION 15
 
 enum {
   GPA_OK = 0,
@@ -84,6 +84,9 @@ size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D
  *   a [B, M, D] bf16 (source metric), b [B, N, D] bf16 (destination metric)
  *   out_max[b*omax_sb + m] = max_n  sum_d a[b,m,d] * b[b,n,d]   (fp32 accumulate)
  *   out_idx[b*oidx_sb + m] = the lowest n attaining that maximum (int64)
+ * out_max holds max_dtype elements: GPA_DTYPE_F32, or GPA_DTYPE_BF16 /
+ * GPA_DTYPE_F16 (the fp32 max rounded to nearest even), so the reference's
+ * `node_max` in a's dtype (fused_similarity.py:112) needs no separate cast.
  * Replaces merging/fused_similarity.py:81-112 (`fused_similarity_argmax`);
  * the index tie rule follows the kernel's strict `>` at
  * merging/fused_similarity.py:73 together with tl.argmax's first index.
@@ -92,7 +95,7 @@ size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D
  * NaN scores never win (an all-NaN row yields -inf and index 0).
  */
 int gpa_sim_argmax_bf16(const void* a, const void* b,
-                        float* out_max, int64_t* out_idx,
+                        void* out_max, int max_dtype, int64_t* out_idx,
                         int64_t B, int64_t M, int64_t N, int64_t D,
                         int64_t a_sb, int64_t a_sm,
                         int64_t b_sb, int64_t b_sn,
@@ -105,7 +108,7 @@ int gpa_sim_argmax_bf16(const void* a, const void* b,
  * the reference passes to its kernel as they are (only an fp32 `a` is cast,
  * to bf16). */
 int gpa_sim_argmax_f16(const void* a, const void* b,
-                       float* out_max, int64_t* out_idx,
+                       void* out_max, int max_dtype, int64_t* out_idx,
                        int64_t B, int64_t M, int64_t N, int64_t D,
                        int64_t a_sb, int64_t a_sm,
                        int64_t b_sb, int64_t b_sn,

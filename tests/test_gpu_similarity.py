@@ -240,3 +240,16 @@ def test_last_round_cut_into_sub_ranges(dev):
     assert np.array_equal(vidx[sure], fidx[sure])
     assert np.array_equal(vidx[0, rows.numpy()], copies[0].numpy())
     assert np.array_equal(fidx[0, rows.numpy()], copies[0].numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_max_written_in_the_input_dtype(dev, dtype):
+    """fused_similarity_argmax returns node_max in a's dtype
+    (merging/fused_similarity.py:112): the kernel writes it in that dtype,
+    bit-identical to casting its fp32 max, with the same indices."""
+    a = _unit_bf16_values((1, 9000, 128), seed=71).to(dtype)
+    b = _unit_bf16_values((1, 30_000, 128), seed=72).to(dtype)
+    vmax, vidx = fused_similarity_argmax(a.to(dev), b.to(dev))
+    fmax, fidx = torch.ops.gpa.sim_argmax(a.to(dev), b.to(dev))
+    assert vmax.dtype == dtype and fmax.dtype == torch.float32
+    assert torch.equal(vmax, fmax.to(dtype)) and torch.equal(vidx, fidx)

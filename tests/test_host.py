@@ -48,7 +48,7 @@ FAKE = 4096  # a 16-byte aligned non-null address; validation returns before any
 
 
 def _sim(**kw):
-    args = dict(a=FAKE, b=FAKE, out_max=FAKE, out_idx=FAKE, B=1, M=10, N=10, D=128,
+    args = dict(a=FAKE, b=FAKE, out_max=FAKE, max_dtype=0, out_idx=FAKE, B=1, M=10, N=10, D=128,
                 a_sb=1280, a_sm=128, b_sb=1280, b_sn=128, omax_sb=10, oidx_sb=10,
                 ws=None, ws_bytes=0, stream=None)
     args.update(kw)
@@ -63,6 +63,7 @@ def _sim(**kw):
     (dict(D=4128, a_sm=4128, b_sn=4128), _native.GPA_E_UNSUPPORTED),
     (dict(a_sm=100), _native.GPA_E_INVALID),
     (dict(a=FAKE + 2), _native.GPA_E_INVALID),
+    (dict(max_dtype=5), _native.GPA_E_INVALID),
     (dict(M=100_000, N=100_000), _native.GPA_E_WORKSPACE),
 ])
 def test_sim_argmax_argument_errors(kw, code):
