@@ -796,6 +796,251 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
   }
 }
 
+// D a multiple of 128, >= 512 (the unprojected 1024-d metric): the GEMM
+// shape at 256 x 128 workgroup tiles.  At 128 x 128 (the kernel above) a
+// 64 x 64 wave tile reads 8 KB of fragments from LDS per 32-feature stage
+// for 16 MFMAs (256 cycles); eight such waves per CU plus the DMA writes ask
+// ~190 bytes per clock of an LDS port that delivers 128, so LDS, not the
+// matrix pipe, sets the pace (23 % of peak).  Here:
+//   * one workgroup per CU, four waves; wave w owns 128 source x 64
+//     destination rows (source half w & 1, destination half w >> 1) as 8 x 4
+//     accumulators of v_mfma_f32_16x16x32 (128 registers, kept in AGPRs),
+//     so each source fragment read from LDS feeds 4 MFMAs and each
+//     destination fragment 8 (12 KB of reads per 32 MFMAs instead of 8 KB
+//     per 16; ~140 bytes per clock with the DMA writes at full MFMA rate);
+//   * 32-feature stages (16 KB of source, 8 KB of destination rows) in a
+//     four-slot ring filled by buffer_load ... lds DMA (six instructions per
+//     wave per stage), two stages in flight, one barrier per stage;
+//   * the fragments of stage s+1 are read from LDS while the 32 MFMAs of
+//     stage s run on the ones read the iteration before (two register sets),
+//     since one wave per SIMD has no second wave to hide the LDS latency;
+//   * rows keep the 64-byte layout and (row >> 2) & 3 chunk swizzle of the
+//     kernel above (conflict-free), so a wave's fragments sit at one base
+//     address plus 1 KB steps (immediate offsets);
+//   * the fold after a destination tile's last stage (one source block at a
+//     time) and the final reductions are those of the kernel above (strict
+//     `>` in destination order per lane, lowest index across lanes and
+//     halves).
+constexpr int kWM = 256;                  // source rows per workgroup tile
+constexpr int kWN = 128;                  // destination rows per workgroup tile
+constexpr int kWRing = 4;
+
+template <bool F16>
+__global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int D) {
+  constexpr int kSA = kWM * 64, kSB_ = kWN * 64;   // stage bytes per operand
+  __shared__ __attribute__((aligned(16))) uint8_t a0[kSA], a1[kSA], a2[kSA], a3[kSA],
+      b0[kSB_], b1[kSB_], b2[kSB_], b3[kSB_];
+  __shared__ float x_best[kWM];
+  __shared__ int x_idx[kWM];
+  uint8_t* const ra[kWRing] = {a0, a1, a2, a3};
+  uint8_t* const rb[kWRing] = {b0, b1, b2, b3};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int quad = lane >> 4, l16 = lane & 15;
+  const int64_t batch = blockIdx.y;
+  int mblock, split;
+  map_block(p, blockIdx.x, mblock, split);
+  mblock = __builtin_amdgcn_readfirstlane(mblock);
+  split = __builtin_amdgcn_readfirstlane(split);
+  const int64_t m_wg = (int64_t)mblock * kWM;
+  if (m_wg >= p.M) return;  // padding block: the whole workgroup leaves together
+
+  const int64_t n_begin = (int64_t)split * p.n_chunk;
+  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
+  const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + kWN - 1) / kWN) : 0;
+  const int nk = D / 32;                   // a multiple of kWRing
+  const int nstages = ntiles * nk;
+
+  const int64_t m_rows = min((int64_t)kWM, p.M - m_wg);
+  const uint32_t a_row = (uint32_t)p.a_sm * 2u, b_row = (uint32_t)p.b_sn * 2u;
+  const __amdgpu_buffer_rsrc_t ars = make_rsrc(p.a + batch * p.a_sb + m_wg * p.a_sm,
+                                               (uint32_t)(((m_rows - 1) * p.a_sm + D) * 2));
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(
+      p.b + batch * p.b_sb + n_begin * p.b_sn,
+      n_end > n_begin ? (uint32_t)(((n_end - n_begin - 1) * p.b_sn + D) * 2) : 0u);
+  // DMA roles: source instruction j of wave w fills rows 64w + 16j .. +16,
+  // destination instruction j rows 32w + 16j .. +16 of a stage; lane l lands
+  // at row +l/4, chunk l%4 and fetches the logical chunk the swizzle puts
+  // there.
+  uint32_t a_voff[4], b_voff[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = wave * 64 + j * 16 + (lane >> 2);
+    a_voff[j] = (uint32_t)row * a_row + (((lane & 3) ^ ((row >> 2) & 3)) * 16);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = wave * 32 + j * 16 + (lane >> 2);
+    b_voff[j] = (uint32_t)row * b_row + (((lane & 3) ^ ((row >> 2) & 3)) * 16);
+  }
+  auto issue = [&](int s, uint8_t* A, uint8_t* Bd) __attribute__((always_inline)) {
+    const int t = s / nk, kc = s - t * nk;
+    const uint32_t ks = (uint32_t)kc * 64u;
+    const uint32_t ts = (uint32_t)t * kWN * b_row + ks;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ars, (__attribute__((address_space(3))) void*)(A + (wave * 64 + j * 16) * 64), 16,
+          a_voff[j], ks, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          brs, (__attribute__((address_space(3))) void*)(Bd + (wave * 32 + j * 16) * 64), 16,
+          b_voff[j], ts, 0, 0);
+  };
+  // Fragment blk of a wave: rows 128 wm + 16 blk + l16 (source), 64 wn + 16
+  // blk + l16 (destination), logical chunk quad; the swizzle term depends on
+  // l16 only.
+  const int swz = (quad ^ ((l16 >> 2) & 3)) << 4;
+  const int s_base = (wm * 128 + l16) * 64 + swz;
+  const int d_base = (wn * 64 + l16) * 64 + swz;
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int sb = 0; sb < 8; ++sb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
+  float best[8];
+  int bidx[8];
+#pragma unroll
+  for (int sb = 0; sb < 8; ++sb) {
+    best[sb] = -INFINITY;
+    bidx[sb] = 0;                          // relative to n_begin until the end
+  }
+
+  bf16x8 fs0[8], fd0[4], fs1[8], fd1[4];
+  auto read = [&](const uint8_t* A, const uint8_t* Bd, bf16x8 (&fs)[8], bf16x8 (&fd)[4])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+      fs[blk] = *reinterpret_cast<const bf16x8*>(A + s_base + blk * 1024);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+      fd[blk] = *reinterpret_cast<const bf16x8*>(Bd + d_base + blk * 1024);
+  };
+  auto mma = [&](const bf16x8 (&fs)[8], const bf16x8 (&fd)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[sb][db] = mfma16x16x32_t<F16>(fd[db], fs[sb], acc[sb][db]);
+  };
+  // Fold the finished scores of destination tile t, then restart the sums:
+  // one source block at a time (a scheduling barrier between them), so that
+  // at most one block's 16 scores leave the accumulator registers at once.
+  // Destination rows past the split end (rel >= lim) never win.  (Every
+  // lambda here is forced inline: a call would put the accumulators it
+  // reaches by reference into scratch memory.)
+  auto fold = [&](int t) __attribute__((always_inline)) {
+    const int base = t * kWN + wn * 64 + 4 * quad;     // relative to n_begin
+    const int lim = (int)(n_end - n_begin);
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rel = base + db * 16 + r;
+          const float v = acc[sb][db][r];
+          const bool upd = v > best[sb] && rel < lim;
+          best[sb] = upd ? v : best[sb];
+          bidx[sb] = upd ? rel : bidx[sb];
+        }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Iteration s: refill the slot of stage s-1 (its fragments were read in
+  // iteration s-2) with stage s+3; wait for stage s+1 (stages s+2, s+3 stay
+  // in flight); barrier; read stage s+1's fragments into the other register
+  // set; the 32 MFMAs of stage s.  (The stages past the end fetch a
+  // destination tile past the split: zeros.)  A destination tile's stages
+  // are whole groups of kWRing (nk is a multiple of it), so the fold follows
+  // a group.
+  auto step = [&](const int s, const int u, auto cur) __attribute__((always_inline)) {
+    constexpr bool C0 = decltype(cur)::value;
+    issue(s + kWRing - 1, ra[(u + kWRing - 1) % kWRing], rb[(u + kWRing - 1) % kWRing]);
+    wait_vm<6 * (kWRing - 2)>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (C0) {
+      read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs1, fd1);
+      mma(fs0, fd0);
+    } else {
+      read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs0, fd0);
+      mma(fs1, fd1);
+    }
+  };
+
+  if (nstages > 0) {
+#pragma unroll
+    for (int i = 0; i < kWRing - 1; ++i) issue(i, ra[i], rb[i]);
+    wait_vm<6 * (kWRing - 2)>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read(ra[0], rb[0], fs0, fd0);
+    for (int s = 0; s < nstages; s += kWRing) {
+      step(s + 0, 0, std::true_type{});
+      step(s + 1, 1, std::false_type{});
+      step(s + 2, 2, std::true_type{});
+      step(s + 3, 3, std::false_type{});
+      if ((s + kWRing) % nk == 0) fold(s / nk);
+    }
+  }
+  wait_vm<0>();
+#pragma unroll
+  for (int sb = 0; sb < 8; ++sb) bidx[sb] += (int)n_begin;
+
+  // Four lanes per source row (quads), lowest index on ties.
+#pragma unroll
+  for (int sb = 0; sb < 8; ++sb) {
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float ov = __shfl_xor(best[sb], sh);
+      const int oi = __shfl_xor(bidx[sb], sh);
+      if (ov > best[sb] || (ov == best[sb] && oi < bidx[sb])) {
+        best[sb] = ov;
+        bidx[sb] = oi;
+      }
+    }
+  }
+  // The second destination half hands its results to the first over LDS.
+  if (wn == 1 && quad == 0) {
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+      x_best[wm * 128 + sb * 16 + l16] = best[sb];
+      x_idx[wm * 128 + sb * 16 + l16] = bidx[sb];
+    }
+  }
+  __syncthreads();
+  if (wn == 0 && quad == 0) {
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+      const int r = wm * 128 + sb * 16 + l16;
+      float bv = best[sb];
+      int bi = bidx[sb];
+      const float ov = x_best[r];
+      const int oi = x_idx[r];
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+      const int64_t m = m_wg + r;
+      if (m < p.M) {
+        if (p.splits == 1) {
+          store_max(p, batch * p.omax_sb + m, bv);
+          p.out_idx[batch * p.oidx_sb + m] = bi;
+        } else {
+          p.part[(batch * p.M + m) * p.splits + split] = part_key(bv, bi);
+        }
+      }
+    }
+  }
+}
+
 // Merge a row's partial keys: the largest key, i.e. the largest max and,
 // among equal maxima, the lowest index -- what the reference's strict `>`
 // across destination tiles keeps.  A row's keys are contiguous, so a wave
@@ -868,10 +1113,16 @@ int device_slots() {
 // Largest feature dim of the GEMM-tiled kernel (D > 256).
 constexpr int64_t kMaxD = 4096;
 
+// Which kernel serves a feature dim: register-resident source rows up to
+// 256, the 256 x 256-tile kernel for multiples of 128 from 512, the
+// 128 x 128-tile kernel for the rest.
+__host__ __device__ constexpr bool wide_dim(int64_t D) { return D >= 512 && D % 128 == 0; }
+
 SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   SimPlan pl{};
   const bool gemm = D > 256;
-  const int rows = gemm ? kGT : rows_per_wg((int)(D / 32));
+  const bool wide = wide_dim(D);
+  const int rows = wide ? kWM : gemm ? kGT : rows_per_wg((int)(D / 32));
   const int64_t mb = (M + rows - 1) / rows;
   // Split the destination range until the grid holds >= 2048 workgroups
   // (8 per CU on 256 CUs) or a split would drop below 512 rows.  Once there
@@ -890,7 +1141,7 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   }
   pl.mblocks = (int)mbp;
   const int64_t per = (N + splits - 1) / splits;
-  const int gran = gemm ? kGT : kTN;      // whole destination tiles per split
+  const int gran = wide ? kWN : gemm ? kGT : kTN;   // whole destination tiles per split
   pl.n_chunk = (per + gran - 1) / gran * gran;
   pl.part_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
   pl.ws_bytes = pl.part_bytes;
@@ -985,10 +1236,11 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
 
   const SimPlan pl = make_plan(B, M, N, D);
   // Buffer offsets are 32-bit: one split of destination rows, plus the
-  // tiles fetched past its end (two stages, or eight 16-row tiles), must
-  // stay below 2^31 bytes.
-  if ((pl.n_chunk + 2 * kTN) * b_sn * 2 >= ((int64_t)1 << 31) ||
-      (int64_t)kGT * a_sm * 2 >= ((int64_t)1 << 31)) {
+  // tiles fetched past its end (two stages, eight 16-row tiles, or one
+  // 256-row tile), and one source block must stay below 2^31 bytes.
+  const int64_t past = wide_dim(D) ? kWN : 2 * kTN, src_rows = wide_dim(D) ? kWM : kGT;
+  if ((pl.n_chunk + past) * b_sn * 2 >= ((int64_t)1 << 31) ||
+      src_rows * a_sm * 2 >= ((int64_t)1 << 31)) {
     gpa_set_error("%s: destination split or source block exceeds 2 GiB (N=%lld, row strides "
                   "%lld / %lld)", fn, (long long)N, (long long)a_sm, (long long)b_sn);
     return GPA_E_UNSUPPORTED;
@@ -1043,7 +1295,10 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
+      if (wide_dim(D))
+        hipLaunchKernelGGL(sim_argmax_wide_kernel<F16>, grid, block, 0, s, p, (int)D);
+      else
+        hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
       break;
   }
   hipError_t e = hipGetLastError();
