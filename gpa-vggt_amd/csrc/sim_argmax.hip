@@ -589,7 +589,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
 //     buffer_load ... lds DMA (four instructions per wave) into a ring of
 //     four stages, three in flight while one is computed; one barrier per
 //     stage.  Rows are 64 bytes with their four 16-byte chunks swizzled by
-//     (row >> 2) & 3, so the 16 lanes reading one chunk of 16 rows hit 16
+//     row_swz(row), so the 16 lanes reading one chunk of 16 rows hit 16
 //     distinct bank groups.
 //   * After the last stage of a destination tile the 64 scores per lane fold
 //     into the lane's running (max, index) per source block, in increasing
@@ -601,6 +601,16 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_d128_kernel(SimArgs p) {
 //     without a break, so the ring keeps streaming across tile boundaries.
 //   * At the end the four lanes of a source row reduce with the lowest-index
 //     rule, and the two destination halves meet in LDS.
+// Chunk swizzle of the 64-byte rows (four 16-byte chunks) of the GEMM-tiled
+// kernels: row r keeps logical chunk c at c ^ row_swz(r), with row_swz =
+// bits 1-2 of r, xor 3 when bit 3 is set.  The lanes of a fragment read take
+// 16 consecutive rows at one logical chunk; any 16 of them land in 16
+// distinct 16-byte bank groups of a 64-bank LDS and any 8 consecutive ones in
+// 8 distinct groups of a 32-bank one.  (The earlier (r >> 2) & 3 was
+// conflict-free only for the first: 4 conflict cycles per LDS instruction
+// measured, SQ_LDS_BANK_CONFLICT.)
+__device__ __forceinline__ int row_swz(int r) { return ((r >> 1) & 3) ^ (((r >> 3) & 1) * 3); }
+
 constexpr int kGT = 128;                 // source and destination rows per tile
 constexpr int kGStage = kGT * 32 * 2;    // bytes of one operand per 32-feature stage
 constexpr int kGRing = 4;
@@ -649,7 +659,7 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int row = wave * 32 + j * 16 + (lane >> 2);
-    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    const int ch = (lane & 3) ^ row_swz(row);
     a_voff[j] = (uint32_t)row * a_row + ch * 16;
     b_voff[j] = (uint32_t)row * b_row + ch * 16;
   }
@@ -672,8 +682,8 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
     const int rs = wm * 64 + blk * 16 + l16, rd = wn * 64 + blk * 16 + l16;
-    s_off[blk] = rs * 64 + ((quad ^ ((rs >> 2) & 3)) << 4);
-    d_off[blk] = rd * 64 + ((quad ^ ((rd >> 2) & 3)) << 4);
+    s_off[blk] = rs * 64 + ((quad ^ row_swz(rs)) << 4);
+    d_off[blk] = rd * 64 + ((quad ^ row_swz(rd)) << 4);
   }
 
   f32x4 acc[4][4];
@@ -810,22 +820,37 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
 //     per 16; ~140 bytes per clock with the DMA writes at full MFMA rate);
 //   * 32-feature stages (16 KB of source, 8 KB of destination rows) in a
 //     four-slot ring filled by buffer_load ... lds DMA (six instructions per
-//     wave per stage), two stages in flight, one barrier per stage;
+//     wave per stage), three stages in flight, one barrier per stage; each
+//     slot is a __shared__ array of its own and each unrolled step names
+//     its slots statically: with one array and a runtime slot index the
+//     compiler cannot tell a fragment read from an in-flight DMA and waits
+//     for every DMA before each read (a six-slot ring built that way ran
+//     29 % slower);
 //   * the fragments of stage s+1 are read from LDS while the 32 MFMAs of
 //     stage s run on the ones read the iteration before (two register sets),
 //     since one wave per SIMD has no second wave to hide the LDS latency;
-//   * rows keep the 64-byte layout and (row >> 2) & 3 chunk swizzle of the
+//   * rows keep the 64-byte layout and row_swz chunk swizzle of the
 //     kernel above (conflict-free), so a wave's fragments sit at one base
 //     address plus 1 KB steps (immediate offsets);
 //   * the fold after a destination tile's last stage (one source block at a
 //     time) and the final reductions are those of the kernel above (strict
 //     `>` in destination order per lane, lowest index across lanes and
-//     halves).
+//     halves);
+//   * up to 64 destination splits (8 per XCD), so the workgroups an XCD
+//     runs together share source blocks as well as destination tiles in L2
+//     (the plan below).
+// What bounds it: each 32-feature stage moves 24 KB from L2 into a CU's LDS
+// for 2.1 MFLOP (87 FLOP per byte, ~45 bytes per clock per CU at the MFMA
+// peak), which the L2 does not sustain on all 256 CUs at once.
 constexpr int kWM = 256;                  // source rows per workgroup tile
 constexpr int kWN = 128;                  // destination rows per workgroup tile
 constexpr int kWRing = 4;
 
-template <bool F16>
+// NK > 0: the stages per destination tile (D / 32) as a constant, so that a
+// tile's stages unroll completely and no accumulator is carried around a
+// loop (the loop form leaves the register allocator copying the 128 sums at
+// every back edge); NK = 0 for other D, a loop over groups of kWRing stages.
+template <bool F16, int NK>
 __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int D) {
   constexpr int kSA = kWM * 64, kSB_ = kWN * 64;   // stage bytes per operand
   __shared__ __attribute__((aligned(16))) uint8_t a0[kSA], a1[kSA], a2[kSA], a3[kSA],
@@ -851,7 +876,7 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   const int64_t n_begin = (int64_t)split * p.n_chunk;
   const int64_t n_end = min(p.N, n_begin + p.n_chunk);
   const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + kWN - 1) / kWN) : 0;
-  const int nk = D / 32;                   // a multiple of kWRing
+  const int nk = NK > 0 ? NK : D / 32;     // a multiple of kWRing
   const int nstages = ntiles * nk;
 
   const int64_t m_rows = min((int64_t)kWM, p.M - m_wg);
@@ -869,17 +894,18 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = wave * 64 + j * 16 + (lane >> 2);
-    a_voff[j] = (uint32_t)row * a_row + (((lane & 3) ^ ((row >> 2) & 3)) * 16);
+    a_voff[j] = (uint32_t)row * a_row + (((lane & 3) ^ row_swz(row)) * 16);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int row = wave * 32 + j * 16 + (lane >> 2);
-    b_voff[j] = (uint32_t)row * b_row + (((lane & 3) ^ ((row >> 2) & 3)) * 16);
+    b_voff[j] = (uint32_t)row * b_row + (((lane & 3) ^ row_swz(row)) * 16);
   }
-  auto issue = [&](int s, uint8_t* A, uint8_t* Bd) __attribute__((always_inline)) {
-    const int t = s / nk, kc = s - t * nk;
-    const uint32_t ks = (uint32_t)kc * 64u;
-    const uint32_t ts = (uint32_t)t * kWN * b_row + ks;
+  auto issue = [&](int t, int kc, uint8_t* A, uint8_t* Bd) __attribute__((always_inline)) {
+    // Wave-uniform offsets (the compiler cannot prove the tile counter
+    // uniform and would otherwise loop over lanes around each load).
+    const uint32_t ks = __builtin_amdgcn_readfirstlane((uint32_t)kc * 64u);
+    const uint32_t ts = __builtin_amdgcn_readfirstlane((uint32_t)t * kWN * b_row + ks);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -894,15 +920,11 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   // Fragment blk of a wave: rows 128 wm + 16 blk + l16 (source), 64 wn + 16
   // blk + l16 (destination), logical chunk quad; the swizzle term depends on
   // l16 only.
-  const int swz = (quad ^ ((l16 >> 2) & 3)) << 4;
+  const int swz = (quad ^ row_swz(l16)) << 4;
   const int s_base = (wm * 128 + l16) * 64 + swz;
   const int d_base = (wn * 64 + l16) * 64 + swz;
 
-  f32x4 acc[8][4];
-#pragma unroll
-  for (int sb = 0; sb < 8; ++sb)
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
+  f32x4 acc[8][4];                         // a tile's first stage starts them
   float best[8];
   int bidx[8];
 #pragma unroll
@@ -921,15 +943,22 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
     for (int blk = 0; blk < 4; ++blk)
       fd[blk] = *reinterpret_cast<const bf16x8*>(Bd + d_base + blk * 1024);
   };
-  auto mma = [&](const bf16x8 (&fs)[8], const bf16x8 (&fd)[4]) __attribute__((always_inline)) {
+  // The 32 MFMAs of a stage; a destination tile's first stage takes a zero
+  // C operand instead of clearing the sums in the fold (with the clearing
+  // there, the register allocator moved the 128 sums between registers at
+  // every loop back edge).
+  auto mma = [&](const bf16x8 (&fs)[8], const bf16x8 (&fd)[4], auto first)
+      __attribute__((always_inline)) {
+    constexpr bool Z = decltype(first)::value;
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) acc[sb][db] = mfma16x16x32_t<F16>(fd[db], fs[sb], acc[sb][db]);
+      for (int db = 0; db < 4; ++db)
+        acc[sb][db] = mfma16x16x32_t<F16>(fd[db], fs[sb], Z ? f32x4{} : acc[sb][db]);
   };
-  // Fold the finished scores of destination tile t, then restart the sums:
-  // one source block at a time (a scheduling barrier between them), so that
-  // at most one block's 16 scores leave the accumulator registers at once.
+  // Fold the finished scores of destination tile t: one source block at a
+  // time (a scheduling barrier between them), so that at most one block's
+  // 16 scores leave the accumulator registers at once.
   // Destination rows past the split end (rel >= lim) never win.  (Every
   // lambda here is forced inline: a call would put the accumulators it
   // reaches by reference into scratch memory.)
@@ -949,45 +978,81 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
           best[sb] = upd ? v : best[sb];
           bidx[sb] = upd ? rel : bidx[sb];
         }
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[sb][db] = f32x4{};
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Iteration s: refill the slot of stage s-1 (its fragments were read in
-  // iteration s-2) with stage s+3; wait for stage s+1 (stages s+2, s+3 stay
-  // in flight); barrier; read stage s+1's fragments into the other register
-  // set; the 32 MFMAs of stage s.  (The stages past the end fetch a
-  // destination tile past the split: zeros.)  A destination tile's stages
-  // are whole groups of kWRing (nk is a multiple of it), so the fold follows
-  // a group.
-  auto step = [&](const int s, const int u, auto cur) __attribute__((always_inline)) {
+  // Stage kc of destination tile t (ring slot u = kc % kWRing): wait for
+  // stage kc+1 (stages kc+2, kc+3 stay in flight); barrier, after which
+  // every wave has read stage kc's fragments, so its slot takes the DMA of
+  // stage kc+4 at once (in the next tile past nk: three steps for a stage
+  // to land); read stage kc+1's fragments into the other register set while
+  // the 32 MFMAs of stage kc run, one read or DMA issue between two MFMAs
+  // (left to itself the scheduler read each fragment just before its first
+  // MFMA and waited for it there).  A tile's stages are whole groups of
+  // kWRing (nk is a multiple of it), so u is a constant in each unrolled
+  // step.  (The stages past the end fetch a destination tile past the
+  // split: zeros.)
+  auto step = [&](const int t, const int kc, const int u, auto cur, auto first)
+      __attribute__((always_inline)) {
     constexpr bool C0 = decltype(cur)::value;
-    issue(s + kWRing - 1, ra[(u + kWRing - 1) % kWRing], rb[(u + kWRing - 1) % kWRing]);
+    __builtin_amdgcn_sched_barrier(0);
     wait_vm<6 * (kWRing - 2)>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    int kn = kc + kWRing, tn = t;
+    if (kn >= nk) {
+      kn -= nk;
+      ++tn;
+    }
+    issue(tn, kn, ra[u], rb[u]);
     if constexpr (C0) {
       read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs1, fd1);
-      mma(fs0, fd0);
+      mma(fs0, fd0, first);
     } else {
       read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs0, fd0);
-      mma(fs1, fd1);
+      mma(fs1, fd1, first);
     }
+    // MFMA (0x008), DS read (0x100), VMEM (0x010): 12 reads and 6 DMA
+    // issues each after an MFMA, then the remaining 14 MFMAs.
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   if (nstages > 0) {
 #pragma unroll
-    for (int i = 0; i < kWRing - 1; ++i) issue(i, ra[i], rb[i]);
-    wait_vm<6 * (kWRing - 2)>();
+    for (int i = 0; i < kWRing; ++i) issue(0, i, ra[i], rb[i]);
+    wait_vm<6 * (kWRing - 1)>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read(ra[0], rb[0], fs0, fd0);
-    for (int s = 0; s < nstages; s += kWRing) {
-      step(s + 0, 0, std::true_type{});
-      step(s + 1, 1, std::false_type{});
-      step(s + 2, 2, std::true_type{});
-      step(s + 3, 3, std::false_type{});
-      if ((s + kWRing) % nk == 0) fold(s / nk);
+    // A loop per destination tile around the stage loop: with one loop and
+    // an `if` for the fold, the compiler predicated the fold into every
+    // group (accumulators read, selected and written back each time).
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    for (int t = 0; t < ntiles; ++t) {
+      step(t, 0, 0, T_{}, T_{});
+      step(t, 1, 1, F_{}, F_{});
+      step(t, 2, 2, T_{}, F_{});
+      step(t, 3, 3, F_{}, F_{});
+#pragma unroll
+      for (int g = kWRing; g < nk; g += kWRing) {
+        step(t, g + 0, 0, T_{}, F_{});
+        step(t, g + 1, 1, F_{}, F_{});
+        step(t, g + 2, 2, T_{}, F_{});
+        step(t, g + 3, 3, F_{}, F_{});
+      }
+      fold(t);
     }
   }
   wait_vm<0>();
@@ -1133,6 +1198,15 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   int splits = 1;
   while (splits < 16 && mb * B * splits < 2048 && N / (splits * 2) >= 512) splits *= 2;
   if (splits > 1 && splits < 8 && N / 8 >= 512) splits = 8;
+  // Wide D: a workgroup re-reads its 256 source rows (512 KB at D = 1024)
+  // for every 128-row destination tile, which no L2 holds for 32 different
+  // blocks.  With k = splits / 8 splits per XCD the 32 workgroups an XCD
+  // runs at once are 32 / k source blocks x k destination ranges, stepping
+  // through their tiles together, so one round fetches 32 / k blocks and k
+  // tiles into L2 instead of 32 blocks and one tile: k = 8 fetches a
+  // quarter.  Keep >= 4 tiles per split.
+  if (wide && splits >= 8)
+    while (splits < 64 && N / (splits * 2) >= 4 * kWN) splits *= 2;
   pl.splits = splits;
   int64_t mbp = mb;
   if (splits > 1 && splits < 8) {
@@ -1295,8 +1369,12 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      if (wide_dim(D))
-        hipLaunchKernelGGL(sim_argmax_wide_kernel<F16>, grid, block, 0, s, p, (int)D);
+      if (D == 1024)
+        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 32>), grid, block, 0, s, p, (int)D);
+      else if (D == 512)
+        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 16>), grid, block, 0, s, p, (int)D);
+      else if (wide_dim(D))
+        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 0>), grid, block, 0, s, p, (int)D);
       else
         hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
       break;
