@@ -64,6 +64,8 @@ struct SimArgs {
   int splits;          // destination splits (1, 2, 4, 8 or a multiple of 8)
   int mblocks;         // source row blocks, padded to the mapping granularity
   int64_t n_chunk;     // destination rows per split (multiple of kTN)
+  int wide_tiles;      // D >= 512: destination tiles of kWN rows; split s
+                       // covers tiles [s * wide_tiles / splits, (s + 1) * ...)
   // The last round's items, cut finer (D = 128, B = 1): the source blocks
   // from tail_mb0 on give each of their splits to tail_sub workgroups of
   // sub_chunk destination rows each, dispatched after the tail_item0 whole
@@ -807,20 +809,19 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
 }
 
 // D a multiple of 128, >= 512 (the unprojected 1024-d metric): the GEMM
-// shape at 256 x 128 workgroup tiles.  At 128 x 128 (the kernel above) a
+// shape at 256 x 256 workgroup tiles.  At 128 x 128 (the kernel above) a
 // 64 x 64 wave tile reads 8 KB of fragments from LDS per 32-feature stage
 // for 16 MFMAs (256 cycles); eight such waves per CU plus the DMA writes ask
 // ~190 bytes per clock of an LDS port that delivers 128, so LDS, not the
 // matrix pipe, sets the pace (23 % of peak).  Here:
-//   * one workgroup per CU, four waves; wave w owns 128 source x 64
-//     destination rows (source half w & 1, destination half w >> 1) as 8 x 4
-//     accumulators of v_mfma_f32_16x16x32 (128 registers, kept in AGPRs),
-//     so each source fragment read from LDS feeds 4 MFMAs and each
-//     destination fragment 8 (12 KB of reads per 32 MFMAs instead of 8 KB
-//     per 16; ~140 bytes per clock with the DMA writes at full MFMA rate);
-//   * 32-feature stages (16 KB of source, 8 KB of destination rows) in a
-//     four-slot ring filled by buffer_load ... lds DMA (six instructions per
-//     wave per stage), three stages in flight, one barrier per stage; each
+//   * one workgroup per CU, four waves; wave w owns 128 source x 128
+//     destination rows (source half w & 1, destination half w >> 1) as 8 x 8
+//     accumulators of v_mfma_f32_16x16x32 (all 256 AGPRs), so each
+//     fragment read from LDS feeds 8 MFMAs (16 KB of reads per 64 MFMAs;
+//     ~95 bytes per clock with the DMA writes at full MFMA rate);
+//   * 32-feature stages (16 KB of source, 16 KB of destination rows) in a
+//     four-slot ring filled by buffer_load ... lds DMA (eight instructions
+//     per wave per stage), three stages in flight, one barrier per stage; each
 //     slot is a __shared__ array of its own and each unrolled step names
 //     its slots statically: with one array and a runtime slot index the
 //     compiler cannot tell a fragment read from an in-flight DMA and waits
@@ -839,17 +840,18 @@ __global__ __launch_bounds__(256, 2) void sim_argmax_gemm_kernel(SimArgs p, int 
 //   * up to 64 destination splits (8 per XCD), so the workgroups an XCD
 //     runs together share source blocks as well as destination tiles in L2
 //     (the plan below).
-// What bounds it: each 32-feature stage moves 24 KB from L2 into a CU's LDS
-// for 2.1 MFLOP (87 FLOP per byte, ~45 bytes per clock per CU at the MFMA
-// peak), which the L2 does not sustain on all 256 CUs at once.
+// What bounds it: each 32-feature stage moves 32 KB from L2 into a CU's LDS
+// for 4.2 MFLOP (131 FLOP per byte, ~30 bytes per clock per CU at the MFMA
+// peak).  With 256 x 128 tiles (24 KB per 2.1 MFLOP, ~45 bytes per clock)
+// the L2 did not keep up on all 256 CUs at once: 39 % of peak at D = 1024.
 constexpr int kWM = 256;                  // source rows per workgroup tile
-constexpr int kWN = 128;                  // destination rows per workgroup tile
+constexpr int kWN = 256;                  // destination rows per workgroup tile
 constexpr int kWRing = 4;
 
-// NK > 0: the stages per destination tile (D / 32) as a constant, so that a
+// NK: the stages per destination tile (D / 32) as a constant, so that a
 // tile's stages unroll completely and no accumulator is carried around a
-// loop (the loop form leaves the register allocator copying the 128 sums at
-// every back edge); NK = 0 for other D, a loop over groups of kWRing stages.
+// loop (a loop over the stages left the register allocator copying the sums
+// at every back edge, and with a runtime count it spills).
 template <bool F16, int NK>
 __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int D) {
   constexpr int kSA = kWM * 64, kSB_ = kWN * 64;   // stage bytes per operand
@@ -873,10 +875,15 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   const int64_t m_wg = (int64_t)mblock * kWM;
   if (m_wg >= p.M) return;  // padding block: the whole workgroup leaves together
 
-  const int64_t n_begin = (int64_t)split * p.n_chunk;
-  const int64_t n_end = min(p.N, n_begin + p.n_chunk);
-  const int ntiles = n_end > n_begin ? (int)((n_end - n_begin + kWN - 1) / kWN) : 0;
-  const int nk = NK > 0 ? NK : D / 32;     // a multiple of kWRing
+  // Split `split` covers whole tiles [t0, t1): the splits differ by at most
+  // one tile, so no XCD is left with empty ones.
+  const int t0 = (int)((int64_t)split * p.wide_tiles / p.splits);
+  const int t1 = (int)((int64_t)(split + 1) * p.wide_tiles / p.splits);
+  const int64_t n_begin = (int64_t)t0 * kWN;
+  const int64_t n_end = min(p.N, (int64_t)t1 * kWN);
+  const int ntiles = n_end > n_begin ? t1 - t0 : 0;
+  constexpr int nk = NK;                   // a multiple of kWRing
+  static_assert(NK % kWRing == 0 && NK >= kWRing, "whole groups of ring slots");
   const int nstages = ntiles * nk;
 
   const int64_t m_rows = min((int64_t)kWM, p.M - m_wg);
@@ -886,19 +893,18 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   const __amdgpu_buffer_rsrc_t brs = make_rsrc(
       p.b + batch * p.b_sb + n_begin * p.b_sn,
       n_end > n_begin ? (uint32_t)(((n_end - n_begin - 1) * p.b_sn + D) * 2) : 0u);
-  // DMA roles: source instruction j of wave w fills rows 64w + 16j .. +16,
-  // destination instruction j rows 32w + 16j .. +16 of a stage; lane l lands
-  // at row +l/4, chunk l%4 and fetches the logical chunk the swizzle puts
-  // there.
-  uint32_t a_voff[4], b_voff[2];
+  // DMA roles: instruction j of wave w fills rows 64w + 16j .. +16 of a
+  // stage's source and destination rows; lane l lands at row +l/4, chunk
+  // l%4 and fetches the logical chunk the swizzle puts there.
+  uint32_t a_voff[4], b_voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = wave * 64 + j * 16 + (lane >> 2);
     a_voff[j] = (uint32_t)row * a_row + (((lane & 3) ^ row_swz(row)) * 16);
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = wave * 32 + j * 16 + (lane >> 2);
+  for (int j = 0; j < 4; ++j) {
+    const int row = wave * 64 + j * 16 + (lane >> 2);
     b_voff[j] = (uint32_t)row * b_row + (((lane & 3) ^ row_swz(row)) * 16);
   }
   auto issue = [&](int t, int kc, uint8_t* A, uint8_t* Bd) __attribute__((always_inline)) {
@@ -912,19 +918,19 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
           ars, (__attribute__((address_space(3))) void*)(A + (wave * 64 + j * 16) * 64), 16,
           a_voff[j], ks, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          brs, (__attribute__((address_space(3))) void*)(Bd + (wave * 32 + j * 16) * 64), 16,
+          brs, (__attribute__((address_space(3))) void*)(Bd + (wave * 64 + j * 16) * 64), 16,
           b_voff[j], ts, 0, 0);
   };
-  // Fragment blk of a wave: rows 128 wm + 16 blk + l16 (source), 64 wn + 16
-  // blk + l16 (destination), logical chunk quad; the swizzle term depends on
-  // l16 only.
+  // Fragment blk of a wave: rows 128 wm + 16 blk + l16 (source), 128 wn +
+  // 16 blk + l16 (destination), logical chunk quad; the swizzle term depends
+  // on l16 only.
   const int swz = (quad ^ row_swz(l16)) << 4;
   const int s_base = (wm * 128 + l16) * 64 + swz;
-  const int d_base = (wn * 64 + l16) * 64 + swz;
+  const int d_base = (wn * 128 + l16) * 64 + swz;
 
-  f32x4 acc[8][4];                         // a tile's first stage starts them
+  f32x4 acc[8][8];                         // a tile's first stage starts them
   float best[8];
   int bidx[8];
 #pragma unroll
@@ -933,43 +939,42 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
     bidx[sb] = 0;                          // relative to n_begin until the end
   }
 
-  bf16x8 fs0[8], fd0[4], fs1[8], fd1[4];
-  auto read = [&](const uint8_t* A, const uint8_t* Bd, bf16x8 (&fs)[8], bf16x8 (&fd)[4])
+  bf16x8 fs0[8], fd0[8], fs1[8], fd1[8];
+  auto read = [&](const uint8_t* A, const uint8_t* Bd, bf16x8 (&fs)[8], bf16x8 (&fd)[8])
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int blk = 0; blk < 8; ++blk) {
       fs[blk] = *reinterpret_cast<const bf16x8*>(A + s_base + blk * 1024);
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
       fd[blk] = *reinterpret_cast<const bf16x8*>(Bd + d_base + blk * 1024);
+    }
   };
-  // The 32 MFMAs of a stage; a destination tile's first stage takes a zero
+  // The 64 MFMAs of a stage; a destination tile's first stage takes a zero
   // C operand instead of clearing the sums in the fold (with the clearing
   // there, the register allocator moved the 128 sums between registers at
   // every loop back edge).
-  auto mma = [&](const bf16x8 (&fs)[8], const bf16x8 (&fd)[4], auto first)
+  auto mma = [&](const bf16x8 (&fs)[8], const bf16x8 (&fd)[8], auto first)
       __attribute__((always_inline)) {
     constexpr bool Z = decltype(first)::value;
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 8; ++db)
         acc[sb][db] = mfma16x16x32_t<F16>(fd[db], fs[sb], Z ? f32x4{} : acc[sb][db]);
   };
   // Fold the finished scores of destination tile t: one source block at a
   // time (a scheduling barrier between them), so that at most one block's
-  // 16 scores leave the accumulator registers at once.
+  // 32 scores leave the accumulator registers at once.
   // Destination rows past the split end (rel >= lim) never win.  (Every
   // lambda here is forced inline: a call would put the accumulators it
   // reaches by reference into scratch memory.)
   auto fold = [&](int t) __attribute__((always_inline)) {
-    const int base = t * kWN + wn * 64 + 4 * quad;     // relative to n_begin
+    const int base = t * kWN + wn * 128 + 4 * quad;    // relative to n_begin
     const int lim = (int)(n_end - n_begin);
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int rel = base + db * 16 + r;
@@ -987,7 +992,7 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   // every wave has read stage kc's fragments, so its slot takes the DMA of
   // stage kc+4 at once (in the next tile past nk: three steps for a stage
   // to land); read stage kc+1's fragments into the other register set while
-  // the 32 MFMAs of stage kc run, one read or DMA issue between two MFMAs
+  // the 64 MFMAs of stage kc run, one read or DMA issue between two MFMAs
   // (left to itself the scheduler read each fragment just before its first
   // MFMA and waited for it there).  A tile's stages are whole groups of
   // kWRing (nk is a multiple of it), so u is a constant in each unrolled
@@ -997,7 +1002,7 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
       __attribute__((always_inline)) {
     constexpr bool C0 = decltype(cur)::value;
     __builtin_amdgcn_sched_barrier(0);
-    wait_vm<6 * (kWRing - 2)>();
+    wait_vm<8 * (kWRing - 2)>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     int kn = kc + kWRing, tn = t;
@@ -1013,26 +1018,26 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
       read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs0, fd0);
       mma(fs1, fd1, first);
     }
-    // MFMA (0x008), DS read (0x100), VMEM (0x010): 12 reads and 6 DMA
-    // issues each after an MFMA, then the remaining 14 MFMAs.
+    // MFMA (0x008), DS read (0x100), VMEM (0x010): 16 reads and 8 DMA
+    // issues each after an MFMA, then the remaining 40 MFMAs.
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
+    for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 40, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   if (nstages > 0) {
 #pragma unroll
     for (int i = 0; i < kWRing; ++i) issue(0, i, ra[i], rb[i]);
-    wait_vm<6 * (kWRing - 1)>();
+    wait_vm<8 * (kWRing - 1)>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     read(ra[0], rb[0], fs0, fd0);
     // A loop per destination tile around the stage loop: with one loop and
@@ -1148,7 +1153,8 @@ __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_
 struct SimPlan {
   int splits;
   int mblocks;       // padded source blocks
-  int64_t n_chunk;
+  int64_t n_chunk;   // destination rows per split (the largest split when wide)
+  int wide_tiles;    // see SimArgs
   int tail_sub;      // 0: no tail (see SimArgs)
   int tail_mb0;
   int64_t tail_rows;
@@ -1181,7 +1187,11 @@ constexpr int64_t kMaxD = 4096;
 // Which kernel serves a feature dim: register-resident source rows up to
 // 256, the 256 x 256-tile kernel for multiples of 128 from 512, the
 // 128 x 128-tile kernel for the rest.
-__host__ __device__ constexpr bool wide_dim(int64_t D) { return D >= 512 && D % 128 == 0; }
+// D served by sim_argmax_wide_kernel (one instantiation per D; wider D
+// goes to the GEMM-tiled kernel, where a runtime stage count spills).
+__host__ __device__ constexpr bool wide_dim(int64_t D) {
+  return D >= 512 && D <= 1024 && D % 128 == 0;
+}
 
 SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   SimPlan pl{};
@@ -1199,14 +1209,15 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   while (splits < 16 && mb * B * splits < 2048 && N / (splits * 2) >= 512) splits *= 2;
   if (splits > 1 && splits < 8 && N / 8 >= 512) splits = 8;
   // Wide D: a workgroup re-reads its 256 source rows (512 KB at D = 1024)
-  // for every 128-row destination tile, which no L2 holds for 32 different
-  // blocks.  With k = splits / 8 splits per XCD the 32 workgroups an XCD
-  // runs at once are 32 / k source blocks x k destination ranges, stepping
-  // through their tiles together, so one round fetches 32 / k blocks and k
-  // tiles into L2 instead of 32 blocks and one tile: k = 8 fetches a
-  // quarter.  Keep >= 4 tiles per split.
+  // for every destination tile, which no L2 holds for 32 different blocks.
+  // With k = splits / 8 splits per XCD the 32 workgroups an XCD runs at
+  // once are 32 / k source blocks x k destination ranges, stepping through
+  // their tiles together, so one round fetches 32 / k blocks and k tiles
+  // into L2 instead of 32 blocks and one tile: k = 8 fetches a quarter.
+  // Keep >= 3 tiles per split.
+  const int64_t wtiles = (N + kWN - 1) / kWN;
   if (wide && splits >= 8)
-    while (splits < 64 && N / (splits * 2) >= 4 * kWN) splits *= 2;
+    while (splits < 64 && wtiles / (splits * 2) >= 3) splits *= 2;
   pl.splits = splits;
   int64_t mbp = mb;
   if (splits > 1 && splits < 8) {
@@ -1217,6 +1228,12 @@ SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   const int64_t per = (N + splits - 1) / splits;
   const int gran = wide ? kWN : gemm ? kGT : kTN;   // whole destination tiles per split
   pl.n_chunk = (per + gran - 1) / gran * gran;
+  if (wide) {
+    // Near-equal whole-tile ranges (see SimArgs::wide_tiles); n_chunk is
+    // the largest.
+    pl.wide_tiles = (int)wtiles;
+    pl.n_chunk = (wtiles + splits - 1) / splits * kWN;
+  }
   pl.part_bytes = splits > 1 ? (size_t)(B * splits * M) * (sizeof(float) + sizeof(int32_t)) : 0;
   pl.ws_bytes = pl.part_bytes;
   // The last round (D = 128, one batch, whole XCD-mapped splits): when the
@@ -1336,6 +1353,7 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
   p.splits = pl.splits;
   p.mblocks = pl.mblocks;
   p.n_chunk = pl.n_chunk;
+  p.wide_tiles = pl.wide_tiles;
   p.tail_sub = pl.tail_sub;
   p.tail_mb0 = pl.tail_mb0;
   p.tail_rows = pl.tail_rows;
@@ -1369,14 +1387,14 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      if (D == 1024)
-        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 32>), grid, block, 0, s, p, (int)D);
-      else if (D == 512)
-        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 16>), grid, block, 0, s, p, (int)D);
-      else if (wide_dim(D))
-        hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, 0>), grid, block, 0, s, p, (int)D);
-      else
-        hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
+      switch (wide_dim(D) ? D / 32 : 0) {
+#define GPA_SIM_WIDE(nk) \
+  case nk: hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, nk>), grid, block, 0, s, p, (int)D); break;
+        GPA_SIM_WIDE(16) GPA_SIM_WIDE(20) GPA_SIM_WIDE(24) GPA_SIM_WIDE(28) GPA_SIM_WIDE(32)
+#undef GPA_SIM_WIDE
+        default:
+          hipLaunchKernelGGL(sim_argmax_gemm_kernel<F16>, grid, block, 0, s, p, (int)D);
+      }
       break;
   }
   hipError_t e = hipGetLastError();

@@ -43,8 +43,10 @@ def _check(a, b, vmax, vidx):
 @pytest.mark.parametrize("B,M,N,D", [
     (1, 1, 1, 1024), (1, 130, 200, 512), (2, 300, 1000, 1024), (1, 257, 9000, 544),
     (1, 1000, 333, 288), (1, 1024, 12_000, 1024), (3, 129, 129, 768),
-    # 64 destination splits (8 per XCD), the last one empty; B > 1 at D = 512
-    (1, 520, 40_000, 1024), (2, 300, 36_000, 512),
+    # 64 destination splits (8 per XCD); B > 1 at D = 512; every D the
+    # 256 x 256-tile kernel is built for; above 1024 the GEMM-tiled kernel
+    (1, 300, 50_000, 1024), (2, 300, 36_000, 512), (1, 300, 9_000, 640),
+    (1, 257, 9_500, 896), (1, 200, 3_000, 1280),
 ])
 def test_matches_fp64_brute_force(dev, B, M, N, D):
     print(f"[wide sim] B={B} M={M} N={N} D={D}", flush=True)
