@@ -90,8 +90,8 @@ size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D
  * Replaces merging/fused_similarity.py:81-112 (`fused_similarity_argmax`);
  * the index tie rule follows the kernel's strict `>` at
  * merging/fused_similarity.py:73 together with tl.argmax's first index.
- * D must be a multiple of 32 and at most 4096 (above 256 a GEMM-tiled kernel
- * loops over the features: the unprojected 1024-d metric); N >= 1.
+ * D must be a multiple of 32 and at most 4096 (above 256 GEMM-tiled kernels
+ * loop over the features: the unprojected 1024-d metric); N >= 1.
  * NaN scores never win (an all-NaN row yields -inf and index 0).
  */
 int gpa_sim_argmax_bf16(const void* a, const void* b,
