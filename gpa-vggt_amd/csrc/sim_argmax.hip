@@ -882,6 +882,16 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   const int64_t n_begin = (int64_t)t0 * kWN;
   const int64_t n_end = min(p.N, (int64_t)t1 * kWN);
   const int ntiles = n_end > n_begin ? t1 - t0 : 0;
+  // First row of tile t (relative to n_begin): a split holds at least kWN
+  // rows, and its last tile, when the split ends inside it, starts kWN rows
+  // before the end instead, so no tile reaches past n_end.  Rows scored
+  // twice carry the same value and index: the max and the lowest index
+  // attaining it do not change.  (Past the last tile, the prefetch fetches
+  // that tile again.)
+  const int lim_rows = (int)(n_end - n_begin);
+  auto tile_row = [&](int t) __attribute__((always_inline)) {
+    return __builtin_amdgcn_readfirstlane(min(t * kWN, lim_rows - kWN));
+  };
   constexpr int nk = NK;                   // a multiple of kWRing
   static_assert(NK % kWRing == 0 && NK >= kWRing, "whole groups of ring slots");
   const int nstages = ntiles * nk;
@@ -911,7 +921,7 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
     // Wave-uniform offsets (the compiler cannot prove the tile counter
     // uniform and would otherwise loop over lanes around each load).
     const uint32_t ks = __builtin_amdgcn_readfirstlane((uint32_t)kc * 64u);
-    const uint32_t ts = __builtin_amdgcn_readfirstlane((uint32_t)t * kWN * b_row + ks);
+    const uint32_t ts = __builtin_amdgcn_readfirstlane((uint32_t)tile_row(t) * b_row + ks);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -967,21 +977,22 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   // Destination rows past the split end (rel >= lim) never win.  (Every
   // lambda here is forced inline: a call would put the accumulators it
   // reaches by reference into scratch memory.)
+  // Each block's fold is a chain of dependent compares and selects, so two
+  // blocks go together (their chains interleave).  No row is masked: tiles
+  // hold no rows past the split end (tile_row).
   auto fold = [&](int t) __attribute__((always_inline)) {
-    const int base = t * kWN + wn * 128 + 4 * quad;    // relative to n_begin
-    const int lim = (int)(n_end - n_begin);
+    const int base = tile_row(t) + wn * 128 + 4 * quad;    // relative to n_begin
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
-      __builtin_amdgcn_sched_barrier(0);
+      if (sb % 2 == 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int db = 0; db < 8; ++db)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int rel = base + db * 16 + r;
           const float v = acc[sb][db][r];
-          const bool upd = v > best[sb] && rel < lim;
+          const bool upd = v > best[sb];
           best[sb] = upd ? v : best[sb];
-          bidx[sb] = upd ? rel : bidx[sb];
+          bidx[sb] = upd ? base + db * 16 + r : bidx[sb];
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1192,11 +1203,14 @@ constexpr int64_t kMaxD = 4096;
 __host__ __device__ constexpr bool wide_dim(int64_t D) {
   return D >= 512 && D <= 1024 && D % 128 == 0;
 }
+// ... and at least one whole destination tile (every split then holds >= kWN
+// rows: one split, or >= 1,024 rows each).
+__host__ __device__ constexpr bool use_wide(int64_t D, int64_t N) { return wide_dim(D) && N >= kWN; }
 
 SimPlan make_plan(int64_t B, int64_t M, int64_t N, int64_t D) {
   SimPlan pl{};
   const bool gemm = D > 256;
-  const bool wide = wide_dim(D);
+  const bool wide = use_wide(D, N);
   const int rows = wide ? kWM : gemm ? kGT : rows_per_wg((int)(D / 32));
   const int64_t mb = (M + rows - 1) / rows;
   // Split the destination range until the grid holds >= 2048 workgroups
@@ -1329,7 +1343,7 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
   // Buffer offsets are 32-bit: one split of destination rows, plus the
   // tiles fetched past its end (two stages, eight 16-row tiles, or one
   // 256-row tile), and one source block must stay below 2^31 bytes.
-  const int64_t past = wide_dim(D) ? kWN : 2 * kTN, src_rows = wide_dim(D) ? kWM : kGT;
+  const int64_t past = use_wide(D, N) ? kWN : 2 * kTN, src_rows = use_wide(D, N) ? kWM : kGT;
   if ((pl.n_chunk + past) * b_sn * 2 >= ((int64_t)1 << 31) ||
       src_rows * a_sm * 2 >= ((int64_t)1 << 31)) {
     gpa_set_error("%s: destination split or source block exceeds 2 GiB (N=%lld, row strides "
@@ -1387,7 +1401,7 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
     GPA_SIM_CASE(5) GPA_SIM_CASE(6) GPA_SIM_CASE(7) GPA_SIM_CASE(8)
 #undef GPA_SIM_CASE
     default:
-      switch (wide_dim(D) ? D / 32 : 0) {
+      switch (use_wide(D, N) ? D / 32 : 0) {
 #define GPA_SIM_WIDE(nk) \
   case nk: hipLaunchKernelGGL((sim_argmax_wide_kernel<F16, nk>), grid, block, 0, s, p, (int)D); break;
         GPA_SIM_WIDE(16) GPA_SIM_WIDE(20) GPA_SIM_WIDE(24) GPA_SIM_WIDE(28) GPA_SIM_WIDE(32)
