@@ -99,8 +99,8 @@ def test_ties_resolve_to_lowest_index(dev, N):
 def test_rows_past_n_never_win(dev, M, N):
     """b as a view of the first N rows of a larger buffer whose next rows are
     100x the source rows (each would beat every real score of its source
-    row): the kernel fetches whole 128-row tiles and three stages past the
-    end of each split, and those rows must neither win nor move the max."""
+    row): the kernels fetch whole tiles and stages ahead of the one they
+    score, and rows past N must neither win nor move the max."""
     a = _unit_values((1, M, 1024), seed=M + N)
     b = _unit_values((1, N, 1024), seed=M + N + 1)
     big = torch.cat([b, 100 * a, torch.zeros(1, 256, 1024)], dim=1)
@@ -111,6 +111,32 @@ def test_rows_past_n_never_win(dev, M, N):
     assert np.abs(vmax.float().cpu().numpy() - fmax).max() < 4e-3          # bf16 output dtype
     sure = gap > 1e-5
     assert np.array_equal(vidx.cpu().numpy()[sure], fidx[sure])
+
+
+@pytest.mark.parametrize("N", [1000, 40_000])
+def test_last_tile_rows_scored_twice(dev, N):
+    """A split that ends inside a 256-row tile has its last tile start 256
+    rows before its end, so that tile's first rows (N - 256 on) were scored
+    by the tile before too.  Maxima planted there, each with an exact copy
+    later in the last tile, must report the first copy; maxima planted only
+    in the last tile's own rows report theirs.  (N = 1000: one split, rows
+    744..767 scored twice; N = 40,000: 32 splits, the last one 38,912 ..
+    39,999, rows 39,744..39,935 scored twice.)"""
+    print(f"[wide sim] overlap N={N}", flush=True)
+    a = _unit_values((1, 48, 1024), seed=N + 3)
+    b = _unit_values((1, N, 1024), seed=N + 4)
+    want = []
+    for i in range(24):                     # in the rows scored twice, a copy at N-1-i
+        b[0, N - 256 + i] = a[0, i]
+        b[0, N - 1 - i] = a[0, i]
+        want.append(N - 256 + i)
+    for i in range(24, 48):                 # once, in the last tile's own rows
+        b[0, N - 1 - i] = a[0, i]
+        want.append(N - 1 - i)
+    vmax, vidx = fused_similarity_argmax(a.to(dev), b.to(dev))
+    assert vidx[0].cpu().tolist() == want
+    fmax, _, _ = sim_argmax_fp64(a, b)
+    assert np.abs(vmax.float().cpu().numpy() - fmax).max() < 1e-5
 
 
 def test_strided_views(dev):
