@@ -57,9 +57,12 @@ def test_matches_fp64_brute_force(dev, B, M, N, D):
     _check(a, b, vmax, vidx)
 
 
-def test_fp16_operands(dev):
-    a = _unit_values((1, 700, 1024), seed=1, dtype=torch.float16)
-    b = _unit_values((1, 5000, 1024), seed=2, dtype=torch.float16)
+@pytest.mark.parametrize("D", [512, 640, 768, 896, 1024])
+def test_fp16_operands(dev, D):
+    """Every D the 256 x 256-tile kernel is built for, on fp16 operands."""
+    print(f"[wide sim] fp16 D={D}", flush=True)
+    a = _unit_values((1, 700, D), seed=1 + D, dtype=torch.float16)
+    b = _unit_values((1, 5000, D), seed=2 + D, dtype=torch.float16)
     vmax, vidx = fused_similarity_argmax(a.to(dev).half(), b.to(dev).half())
     assert vmax.dtype == torch.float16
     s = a.double().numpy()[0] @ b.double().numpy()[0].T       # fp64 on the fp16 values
