@@ -1003,9 +1003,10 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
   // every wave has read stage kc's fragments, so its slot takes the DMA of
   // stage kc+4 at once (in the next tile past nk: three steps for a stage
   // to land); read stage kc+1's fragments into the other register set while
-  // the 64 MFMAs of stage kc run, one read or DMA issue between two MFMAs
-  // (left to itself the scheduler read each fragment just before its first
-  // MFMA and waited for it there).  A tile's stages are whole groups of
+  // the 64 MFMAs of stage kc run, the reads and DMA issues spread over the
+  // whole stage (left to itself the scheduler read each fragment just before
+  // its first MFMA and waited for it there; all 24 issued within the first
+  // 24 MFMAs measured 7 % slower than spread, same box).  A tile's stages are whole groups of
   // kWRing (nk is a multiple of it), so u is a constant in each unrolled
   // step.  (The stages past the end fetch a destination tile past the
   // split: zeros.)
@@ -1029,19 +1030,18 @@ __global__ __launch_bounds__(256, 1) void sim_argmax_wide_kernel(SimArgs p, int 
       read(ra[(u + 1) % kWRing], rb[(u + 1) % kWRing], fs0, fd0);
       mma(fs1, fd1, first);
     }
-    // MFMA (0x008), DS read (0x100), VMEM (0x010): 16 reads and 8 DMA
-    // issues each after an MFMA, then the remaining 40 MFMAs.
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+    // MFMA (0x008), DS read (0x100), VMEM (0x010): eight groups of eight
+    // MFMAs, each carrying two of the 16 reads and one of the 8 DMA issues.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 40, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
