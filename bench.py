@@ -435,7 +435,7 @@ def main(argv=None) -> int:
                 "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
         del qkv
         # The unprojected metric (metric_dim=0, D = 1024) at the 200-frame
-        # shape: the GEMM-tiled similarity kernel.
+        # shape: the 256 x 256-tile similarity kernel.
         s3, d3 = W.sim_inputs(m=207_955, n=66_845, out_dim=1024, seed=4, device=dev)
         fn = lambda: fused_similarity_argmax(s3, d3)  # noqa: E731
         fn()

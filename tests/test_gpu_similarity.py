@@ -120,7 +120,7 @@ def test_nan_and_zero_rows(dev, D, half):
     against everything and yields -inf with index 0; destination rows
     holding a NaN are never chosen; an all-zero source row scores 0 against
     every other row and takes index 0.  Covers the register-staged (D 96),
-    pipelined (D 128, bf16 and fp16 operands) and GEMM-tiled (D 512)
+    pipelined (D 128, bf16 and fp16 operands) and 256 x 256-tile (D 512)
     kernels, with several destination splits."""
     M, N = 600, 3000
     a = _unit_bf16_values((1, M, D), seed=71 + D)

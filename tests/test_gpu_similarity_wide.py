@@ -1,5 +1,6 @@
-"""The similarity-argmax above D = 256: the GEMM-tiled kernel that loops over
-the features (the unprojected 1024-d metric of `metric_dim=0`,
+"""The similarity-argmax above D = 256: the GEMM-tiled kernels that loop over
+the features, 256 x 256 tiles for D = 512 ... 1024 in steps of 128 and
+128 x 128 otherwise (the unprojected 1024-d metric of `metric_dim=0`,
 eval/eval_co3d.py:121-122 and merging/merge.py:180, which the reference
 kernel serves by tiling D with BLOCK_K, merging/fused_similarity.py:55-68).
 
