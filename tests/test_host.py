@@ -90,6 +90,13 @@ def test_workspace_bytes():
     # rows) halved
     assert lib.gpa_sim_argmax_workspace_bytes(1, 207_955, 66_845, 128) == \
         8 * 207_955 * 8 + 8 * 2 * 11_347 * 8
+    # D = 1024 (256 x 256 tiles): 200 frames have 262 tiles of 256
+    # destination rows, split 64 ways (8 per XCD, 4-5 tiles each);
+    # 75,000 x 25,000 (98 tiles) 32 ways; N < 256 runs the 128 x 128 kernel
+    # without splits here
+    assert lib.gpa_sim_argmax_workspace_bytes(1, 207_955, 66_845, 1024) == 8 * 207_955 * 64
+    assert lib.gpa_sim_argmax_workspace_bytes(1, 75_000, 25_000, 1024) == 8 * 75_000 * 32
+    assert lib.gpa_sim_argmax_workspace_bytes(1, 300, 200, 1024) == 0
 
 
 def _attn(**kw):
