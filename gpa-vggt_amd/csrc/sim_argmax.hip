@@ -1140,10 +1140,12 @@ __global__ __launch_bounds__(256) void sim_argmax_merge_kernel(SimArgs p, int64_
   constexpr int kBatch = 16;
   for (int s0 = 0; s0 < parts; s0 += kBatch) {
     uint64_t v[kBatch];
-    if (s0 + kBatch <= parts && parts % 2 == 0) {
+    if (parts % 2 == 0) {                  // 16-byte aligned pairs (also a short batch)
+      const int n = min(kBatch, parts - s0);
 #pragma unroll
       for (int u = 0; u < kBatch; u += 2) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(k + s0 + u);
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (u < n) w = *reinterpret_cast<const u32x4*>(k + s0 + u);
         v[u] = ((uint64_t)w[1] << 32) | w[0];
         v[u + 1] = ((uint64_t)w[3] << 32) | w[2];
       }
