@@ -185,6 +185,62 @@ def event_ms(fn, reps: int):
     return [s.elapsed_time(e) for s, e in out]
 
 
+def attention_floor(q, k, v, bias, biased_ms: float) -> dict:
+    """The unbiased floor of the headline attention on this box, measured
+    the way the reference judges its own kernel (merging/fused_attention.py:
+    23-25: the biased kernel against a flash kernel without bias).
+
+    * this kernel with bias=None on the same q, k, v;
+    * torch's unmasked F.scaled_dot_product_attention, restricted to one
+      fused backend at a time (flash, then memory-efficient; the math
+      backend is never allowed: it would materialise a 274,800 x 68,700
+      score matrix per head);
+    * torch's masked SDPA with the same log-count bias, the reference's
+      own GPU fallback (vggt/layers/attention.py:270-276).
+    Each entry: ms, TFLOP/s, % of peak, and biased_ms / its ms.
+    """
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import gpa_workloads as W
+    from merging.fused_attention import attention_keybias
+
+    f = W.attn_flops(q.shape[1], q.shape[2], k.shape[2], q.shape[3])
+    out = {}
+
+    def entry(name, fn, reps=3, **extra):
+        try:
+            fn()
+            t = statistics.median(event_ms(fn, reps))
+        except RuntimeError as e:       # backend not built for this device / shape
+            out[name] = {"error": str(e).splitlines()[0][:200]}
+            log(f"[bench] {name}: unavailable ({out[name]['error']})")
+            return
+        ent = kernel_entry(f, t)
+        ent["biased_over_this"] = round(biased_ms / t, 4)
+        ent.update(extra)
+        out[name] = ent
+        log(f"[bench] {name}: {t:.2f} ms")
+
+    entry("gpa_attn_no_bias", lambda: attention_keybias(q, k, v, None, SM_SCALE))
+    for be, tag in ((SDPBackend.FLASH_ATTENTION, "flash"),
+                    (SDPBackend.EFFICIENT_ATTENTION, "efficient")):
+        def sdpa(be=be):
+            with sdpa_kernel([be]):
+                return F.scaled_dot_product_attention(q, k, v, scale=SM_SCALE)
+        entry(f"torch_sdpa_unmasked_{tag}", sdpa, backend=str(be))
+    def sdpa_masked():
+        # [B, H, 1, N], broadcast over the queries, as the reference passes it
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=bias, scale=SM_SCALE)
+    entry("torch_sdpa_masked_efficient", sdpa_masked, backend=str(SDPBackend.EFFICIENT_ATTENTION))
+    torch.cuda.empty_cache()
+    nb = out.get("gpa_attn_no_bias", {})
+    if "ms" in nb:
+        out["bias_overhead_pct"] = round(100.0 * (biased_ms / nb["ms"] - 1.0), 2)
+    return out
+
+
 def kernel_entry(flops: float, ms: float) -> dict:
     tf = flops / (ms * 1e-3) / 1e12
     return {"ms": round(ms, 4), "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
@@ -321,6 +377,8 @@ def main(argv=None) -> int:
     fn()
     kernels["sim_argmax_75000x25000x128_back_to_back"] = kernel_entry(
         f_sim, statistics.median(event_ms(fn, 20)))
+
+    floor = attention_floor(q, k, v, bias, attn_ms)
 
     if not args.no_200f:
         # Reference defaults at 200 frames x 1374 tokens: 207,955 source and
@@ -561,6 +619,7 @@ def main(argv=None) -> int:
                                 "x 274800 queries x 68700 merged keys x d64 (200 frames x 1374 tokens)"),
                    "sm_scale": SM_SCALE, "bias": "log(count), bf16, [1,16,1,N]"},
         "kernels": kernels,
+        "attention_floor": floor,
         "mfma_ceiling": ceiling,
         "e2e": e2e,
         "roofline": roofline,

@@ -46,8 +46,8 @@ HIPCC_FLAGS = [
 
 
 # Per-source extra flags.  The attention kernel keeps its MFMA accumulators
-# in VGPRs with the VGPR form of MFMA selected (195 VGPRs, no AGPR copies or
-# spills at two waves per SIMD).
+# in VGPRs with the VGPR form of MFMA selected (256 VGPRs at two waves per
+# SIMD, no AGPR copies, no VGPR or SGPR spills, no scratch).
 FILE_FLAGS = {
     "attn_keybias.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
@@ -69,6 +69,40 @@ def _compile(src: Path, report: bool) -> tuple[Path, str]:
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
     return obj, res.stderr
+
+
+def resource_usage(sources=None) -> dict:
+    """Per-kernel register and scratch use as hipcc reports it for the
+    library's own flags: {source name: {kernel: {"vgprs", "sgpr_spill",
+    "vgpr_spill", "scratch", "occupancy"}}}.  Compiles to a temporary
+    object; nothing under the package is touched."""
+    import re
+    import tempfile
+    keys = {"VGPRs": "vgprs", "SGPRs Spill": "sgpr_spill", "VGPRs Spill": "vgpr_spill",
+            "ScratchSize [bytes/lane]": "scratch", "Occupancy [waves/SIMD]": "occupancy"}
+    srcs = sorted(CSRC.glob("*.hip")) if sources is None else [CSRC / s for s in sources]
+
+    def one(src: Path):
+        with tempfile.TemporaryDirectory() as tmp:
+            cmd = [_hipcc(), "-Rpass-analysis=kernel-resource-usage", *HIPCC_FLAGS,
+                   *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(Path(tmp) / "k.o")]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
+        kernels, cur = {}, None
+        for line in res.stderr.splitlines():
+            m = re.search(r"remark: (.*?): (\S+) \[-Rpass-analysis", line)
+            if not m:
+                continue
+            name, val = m.group(1).strip(), m.group(2)
+            if name == "Function Name":
+                cur = kernels.setdefault(val, {})
+            elif cur is not None and name in keys:
+                cur[keys[name]] = int(val)
+        return src.name, kernels
+
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        return dict(pool.map(one, srcs))
 
 
 def build(report: bool = False, verbose: bool = True) -> Path:

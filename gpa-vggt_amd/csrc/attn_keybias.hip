@@ -426,6 +426,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   const uint16_t* K = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t* V = p.v + b * p.v_sb + h * p.v_sh;
   const float* R = p.recs + (int64_t)bh * (p.rec_bytes / 4);
+  // The output bases, formed here so that only two pointers (not five
+  // 64-bit strides) stay live in SGPRs until the epilogue.
+  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+  float* LSE = p.lse ? p.lse + b * p.lse_sb + h * p.lse_sh : nullptr;
+  const int o_sm = (int)p.o_sm;
+  asm volatile("" : "+s"(O), "+s"(LSE));
 
   // Q^T as the B-operand of S^T = K . Q^T: in block j the lane supplies
   // query q_base + 32 j, features 16*ks + 8*hi .. +8.  Only the loads here:
@@ -598,45 +604,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   // carries its share of every tile's DMA: the same DMAs, waits and barriers
   // as a live wave, no MFMA or softmax work, so the live wave sharing its
   // SIMD gets the matrix pipe to itself.  Wave-uniform branch, taken before
-  // the live path starts.
-  if ((int64_t)qb * kQPerWG + wave * kQPerWave >= p.M) {
-    auto stream_only = [&]() {
+  // the live path starts.  Should the workgroup stream the keys a second
+  // time (see the verification below), such a wave takes the live waves'
+  // recompute path on its zero-filled queries, whose rows are never stored:
+  // a second copy of the stream loop here costs the whole kernel SGPR and
+  // VGPR spills.
+  const bool dead = (int64_t)qb * kQPerWG + wave * kQPerWave >= p.M;
+  bool fixed = false, opt = false;
+  if (dead) {
 #pragma unroll
-      for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
-      wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
-      tile_barrier();
+    for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
+    wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
+    tile_barrier();
+    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    tile_barrier();
+    auto carry = [&](const int t, MainTile& Tissue) {
+      issue(t + kMainAhead, Tissue);
       wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
       tile_barrier();
-      auto carry = [&](const int t, MainTile& Tissue) {
-        issue(t + kMainAhead, Tissue);
-        wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
-        tile_barrier();
-      };
-      int t = 0;
-      for (; t + kMainSlots <= ntiles; t += kMainSlots) {
-#pragma unroll
-        for (int u = 0; u < kMainSlots; ++u) carry(t + u, *ring[(u + kMainAhead) % kMainSlots]);
-      }
-#pragma unroll
-      for (int u = 0; u < kMainSlots - 1; ++u)
-        if (t < ntiles) {
-          carry(t, *ring[(u + kMainAhead) % kMainSlots]);
-          ++t;
-        }
-      wait_vm<0>();
     };
-    stream_only();
-    // The workgroup's verdict on the tile-0 offsets (see the live path):
-    // if any wave overflowed, every wave streams the keys a second time.
-    if (lane == 0) wg_fail[wave] = 0;
-    tile_barrier();
-    const bool rerun = __builtin_amdgcn_readfirstlane(wg_fail[0] | wg_fail[1] | wg_fail[2] |
-                                                      wg_fail[3]) != 0;
-    if (rerun) stream_only();
-    if (lane == 0) flag_row[wave] = rerun ? 4 : 0;
-    return;
-  }
-
+    int t = 0;
+    for (; t + kMainSlots <= ntiles; t += kMainSlots) {
+#pragma unroll
+      for (int u = 0; u < kMainSlots; ++u) carry(t + u, *ring[(u + kMainAhead) % kMainSlots]);
+    }
+#pragma unroll
+    for (int u = 0; u < kMainSlots - 1; ++u)
+      if (t < ntiles) {
+        carry(t, *ring[(u + kMainAhead) % kMainSlots]);
+        ++t;
+      }
+  } else {
   // Prologue: tiles 0 .. kMainAhead-1 in flight behind the Q loads; |q|;
   // S(0) and the certification.
 #pragma unroll
@@ -666,8 +664,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     bad = bad || !(x0s[j] >= m_off[j] - kDown<F16>);     // NaN scores fail too
   }
   // (Without the key maxima there is no bound to certify anything with.)
-  const bool fixed = !p.no_bound && __builtin_amdgcn_ballot_w64(bad) == 0;
-  bool opt = false;
+  fixed = !p.no_bound && __builtin_amdgcn_ballot_w64(bad) == 0;
   if (!fixed) {
     // The tile-0 offset, taken where tile 0's scores are narrow and no key
     // stands out (so that an overflow is unlikely); verified after the loop.
@@ -691,6 +688,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   }
   wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
   tile_barrier();
+  }
 
   // Iteration t: refill the slot of tile t-1 with tile t+kMainAhead; S(t+1)
   // beside the softmax of S(t); P.V of tile t; tile t+2 lands by its end.
@@ -766,10 +764,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
         ++t;
       }
   };
-  if (fixed || opt)
-    run(std::false_type{});
-  else
-    run(std::true_type{});
+  if (!dead) {
+    if (fixed || opt)
+      run(std::false_type{});
+    else
+      run(std::true_type{});
+  }
   // Drain the DMAs still in flight (before the ring is reused or the
   // workgroup exits).
   wait_vm<0>();
@@ -815,7 +815,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     tile_barrier();
   }
   // Flag bits: 1 = the output comes from the lazily moved offset, 2 = the
-  // wave took the tile-0 offset, 4 = its workgroup streamed the keys twice.
+  // wave took the tile-0 offset, 4 = its workgroup streamed the keys twice
+  // (a wave without queries: 0 or 4).
+  if (dead) {
+    if (lane == 0) flag_row[wave] = rerun ? 4 : 0;
+    return;
+  }
   if (lane == 0)
     flag_row[wave] = (uint8_t)((rerun || !(fixed || opt) ? 1 : 0) | (opt ? 2 : 0) | (rerun ? 4 : 0));
 
@@ -848,12 +853,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
         *reinterpret_cast<bf16x4*>(&stage[r * kHD + ((cw ^ (r & 7)) << 3) + 4 * hi]) = ov;
       }
     const int64_t row = q_base + 32 * j;
-    if (p.lse && hi == 0 && row < p.M)
-      p.lse[b * p.lse_sb + h * p.lse_sh + row] = m_off[j] + __log2f(l_tot);
+    if (LSE && hi == 0 && row < p.M) LSE[row] = m_off[j] + __log2f(l_tot);
   }
   // All eight row reads first, then the stores (read-wait-store in turn
   // serialised eight LDS round trips).
-  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
   const int64_t row0 = (int64_t)qb * kQPerWG + wave * kQPerWave;
   const int ch = lane & 7;
   constexpr int kRowSets = kQPerWave / 8;
@@ -867,14 +870,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < kRowSets; ++i) {
       const int64_t row = row0 + 8 * i + (lane >> 3);
-      if (row < p.M) *reinterpret_cast<u32x4*>(O + row * p.o_sm + ch * 8) = ov16[i];
+      if (row < p.M) *reinterpret_cast<u32x4*>(O + row * o_sm + ch * 8) = ov16[i];
     }
   } else {
 #pragma unroll
     for (int i = 0; i < kRowSets; ++i) {
       const int64_t row = row0 + 8 * i + (lane >> 3);
       if (row < p.M) {
-        u32x2* dst = reinterpret_cast<u32x2*>(O + row * p.o_sm + ch * 8);
+        u32x2* dst = reinterpret_cast<u32x2*>(O + row * o_sm + ch * 8);
         dst[0] = u32x2{ov16[i][0], ov16[i][1]};
         dst[1] = u32x2{ov16[i][2], ov16[i][3]};
       }
@@ -957,6 +960,10 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
     gpa_set_error("%s: rows must have unit feature stride, q/k/v rows "
                   "16-byte and o rows 8-byte aligned", fn);
     return GPA_E_INVALID;
+  }
+  if (o_sm > 0x7fffffffLL) {
+    gpa_set_error("%s: output row stride %lld exceeds 2^31 elements", fn, (long long)o_sm);
+    return GPA_E_UNSUPPORTED;
   }
   if (B * H > 65535) {
     gpa_set_error("%s: B*H=%lld exceeds the grid limit", fn, (long long)(B * H));

@@ -1376,8 +1376,9 @@ int sim_argmax_run(const char* fn, const void* a, const void* b, void* out_max, 
   p.sub_chunk = pl.sub_chunk;
   p.tail_item0 = pl.tail_mb0 * pl.splits;
   if (pl.splits > 1) {
-    if (!workspace || workspace_bytes < pl.ws_bytes) {
-      gpa_set_error("%s: workspace of %zu bytes required, %zu given", fn,
+    // The partial-key merge reads the workspace 16 bytes at a time.
+    if (!workspace || workspace_bytes < pl.ws_bytes || (uintptr_t)workspace % 16) {
+      gpa_set_error("%s: 16-byte aligned workspace of %zu bytes required, %zu given", fn,
                     pl.ws_bytes, workspace ? workspace_bytes : (size_t)0);
       return GPA_E_WORKSPACE;
     }

@@ -264,9 +264,11 @@ def sim_argmax(a: torch.Tensor, b: torch.Tensor,
     if B == 0 or M == 0:
         return out_max, out_idx
     L = lib()
-    ws_bytes = L.gpa_sim_argmax_workspace_bytes(B, M, N, D)
-    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(dev):
+        # The plan (and so the workspace size) depends on the current
+        # device's CU count: query it with the launch's device current.
+        ws_bytes = L.gpa_sim_argmax_workspace_bytes(B, M, N, D)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
         fn = L.gpa_sim_argmax_f16 if a.dtype == torch.float16 else L.gpa_sim_argmax_bf16
         rc = fn(
             a.data_ptr(), b.data_ptr(), out_max.data_ptr(), _DTYPE_CODES[max_dtype],

@@ -38,9 +38,12 @@
  *     legacy default stream).  Functions return GPA_OK (0) after a successful
  *     launch or a negative GPA_E* code; gpa_last_error() then holds a
  *     message for the calling thread.
- *   - The library is stateless and reentrant (except for the shared scratch
- *     of gpa_attn_keybias_bf16_noalloc): tile shapes are a deterministic
- *     function of the problem shape (no autotuning, no global caches).
+ *   - The library is reentrant and keeps no per-call state (except for the
+ *     shared scratch of gpa_attn_keybias_bf16_noalloc): tile shapes are a
+ *     deterministic function of the problem shape and, for the similarity,
+ *     of the current device's CU count (read once per device and cached;
+ *     query gpa_sim_argmax_workspace_bytes with the launch's device
+ *     current).  No autotuning.
  */
 #ifndef GPA_MI355X_H
 #define GPA_MI355X_H
@@ -75,8 +78,9 @@ int gpa_abi_version(void);
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* gpa_last_error(void);
 
-/* Bytes of device workspace gpa_sim_argmax_bf16 needs for this shape
- * (0 when the kernel writes its outputs directly). */
+/* Bytes of device workspace gpa_sim_argmax_bf16 needs for this shape on
+ * the current device (0 when the kernel writes its outputs directly).  The
+ * workspace passed to the call must be 16-byte aligned. */
 size_t gpa_sim_argmax_workspace_bytes(int64_t B, int64_t M, int64_t N, int64_t D);
 
 /*

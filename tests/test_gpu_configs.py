@@ -20,11 +20,13 @@
   - the attention output on 64 sampled query rows x 16 heads against the
     oracle over all 33,945 merged keys (max-abs <= 2e-2, mean-abs <= 2e-3).
 * The whole 200-frame aggregator (DINOv2 patch embed, 24 frame + 24 global
-  blocks on the reference's default GPA schedule): finite outputs of the
-  DPT shapes, bit-identical on a second forward, and for every merged block
-  the slot count (66,845, or 219,840 in the core blocks 13-16), sizes
-  summing to 274,800, and every frame-special pooling's group sizes summing
-  to the 1,369 patches of each frame.
+  blocks), on the reference's default GPA schedule and on the schedule the
+  200-frame workload states (64 pooled summaries per frame, 25 % keep in
+  every merged block): finite outputs of the DPT shapes, bit-identical on a
+  second forward, and for every merged block the slot count (66,845, or
+  219,840 in the core blocks 13-16), sizes summing to 274,800, and every
+  frame-special pooling's group sizes summing to the 1,369 patches of each
+  frame.
 """
 import numpy as np
 import pytest
@@ -161,15 +163,25 @@ def test_config4_merged_block_100_frames(dev, aggregator):
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
 
 
-def test_config5_aggregator_200_frames(dev, aggregator):
-    cfg, agg = aggregator
+@pytest.mark.parametrize("schedule", ["reference_defaults", "pool64_keep25"])
+def test_config5_aggregator_200_frames(dev, aggregator, schedule):
+    """`reference_defaults`: 25 pooled seeds per frame (broadcast_pool 8) and
+    80 % keep in the core blocks 13-16 (aggregator.py:76-78).
+    `pool64_keep25`: the workload as the 200-frame config states it, 64
+    pooled patch summaries per frame (pool stride 5) and 25 % keep in every
+    merged block (no core blocks)."""
+    if schedule == "reference_defaults":
+        cfg, agg = aggregator
+    else:
+        cfg = A.GpaConfig(broadcast_pool=5, core_blocks=())
+        agg = A.build_aggregator(cfg, device=dev, seed=0)
     frames = 200
     N = frames * P
     imgs = A.shifted_texture_images(frames, device=dev).to(BF16)
     logs = ([], [])
     outs = []
     for i, log in enumerate(logs):
-        print(f"[config 5] forward {i + 1} of 2 on {frames} frames", flush=True)
+        print(f"[config 5, {schedule}] forward {i + 1} of 2 on {frames} frames", flush=True)
         agg.set_merge_log(log)
         with torch.no_grad(), torch.autocast("cuda", dtype=BF16):
             outs.append(agg(imgs))
@@ -192,8 +204,9 @@ def test_config5_aggregator_200_frames(dev, aggregator):
         assert r["keys"] == want == r["size"].shape[1], r["block"]
         assert r["size"].sum().item() == N and r["size"].min().item() >= 1
         assert r["slot_offsets"][-1].item() == N
-    assert {r["keys"] for r in merged} == {66_845, 219_840}
+    assert {r["keys"] for r in merged} == ({66_845, 219_840} if cfg.core_blocks else {66_845})
     npool = (-(-GRID // cfg.broadcast_pool)) ** 2
+    assert npool == (25 if cfg.broadcast_pool == 8 else 64)
     for r in pools:
         ps = r["pool_size"]
         assert ps.shape == (1, 16, frames, npool)
@@ -201,6 +214,9 @@ def test_config5_aggregator_200_frames(dev, aggregator):
     for r1, r2 in zip(log1, log2):
         key = "size" if r1["kind"] == "merged" else "pool_size"
         assert torch.equal(r1[key], r2[key])
+    if schedule != "reference_defaults":
+        del agg, outs, out1, out2, logs, log1, log2
+        torch.cuda.empty_cache()
 
 
 def test_config5_fp16_evaluation_stack(dev):

@@ -357,3 +357,33 @@ def test_cpu_tensors_are_refused():
 def test_log2e_constant():
     import math
     assert LOG2E == pytest.approx(1.0 / math.log(2.0), abs=1e-15)
+
+
+def _build_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "gpa_build", Path(__file__).resolve().parent.parent / "gpa-vggt_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_hot_kernels_have_no_spills_or_scratch():
+    """Every kernel of the similarity and attention sources, compiled with
+    the library's own flags, fits its registers: no VGPR or SGPR spills and
+    no scratch (hipcc's kernel-resource-usage report).  The attention kernel
+    must also keep two waves per SIMD."""
+    import shutil
+    b = _build_module()
+    if shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists():
+        pytest.skip("hipcc not available")
+    report = b.resource_usage(["attn_keybias.hip", "sim_argmax.hip"])
+    bad = {}
+    for src, kernels in report.items():
+        assert kernels, f"no kernels reported for {src}"
+        for name, use in kernels.items():
+            if use.get("vgpr_spill") or use.get("sgpr_spill") or use.get("scratch"):
+                bad[f"{src}:{name}"] = use
+    assert not bad, f"kernels with spills or scratch: {bad}"
+    attn = [u for n, u in report["attn_keybias.hip"].items() if "attn_main_kernel" in n]
+    assert len(attn) == 2 and all(u["occupancy"] >= 2 for u in attn), attn

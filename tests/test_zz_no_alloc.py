@@ -38,8 +38,12 @@ def _call(noalloc, q, k, v, bias, o, lse, ws=None):
     B, H, M, D = q.shape
     N = k.shape[2]
     stream = torch.cuda.current_stream(q.device).cuda_stream
-    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), _native.GPA_BIAS_F32,
-            bias.stride(0), bias.stride(1), bias.stride(3), o.data_ptr(), lse.data_ptr(),
+    if bias is None:
+        bias_args = [None, _native.GPA_BIAS_NONE, 0, 0, 0]
+    else:
+        bias_args = [bias.data_ptr(), _native.GPA_BIAS_F32, bias.stride(0), bias.stride(1),
+                     bias.stride(3)]
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), *bias_args, o.data_ptr(), lse.data_ptr(),
             B, H, M, N, D, *_strides(q), *_strides(k), *_strides(v), *_strides(o),
             lse.stride(0), lse.stride(1)]
     if noalloc:
@@ -50,8 +54,10 @@ def _call(noalloc, q, k, v, bias, o, lse, ws=None):
     assert rc == _native.GPA_OK, L.gpa_last_error()
 
 
-def _run_pair(dev, B, H, M, N, q_scale, seed):
+def _run_pair(dev, B, H, M, N, q_scale, seed, with_bias=True):
     q, k, v, bias = _inputs(dev, B, H, M, N, q_scale, seed)
+    if not with_bias:
+        bias = None
     ws_bytes = _native.lib().gpa_attn_keybias_workspace_bytes(B, H, M, N)
     assert 0 < ws_bytes <= _native.NOALLOC_SCRATCH_BYTES
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
@@ -74,3 +80,11 @@ def test_noalloc_matches_allocating_entry_point_twice(dev):
     print("[no-alloc] call 2: B=1 H=2 M=700 N=333, smaller", flush=True)
     _run_pair(dev, 1, 2, 700, 333, 0.5, 1)
 
+
+def test_noalloc_without_bias_after_biased_calls(dev):
+    print("[no-alloc] biased call: B=2 H=4 M=3000 N=2100, sharp logits", flush=True)
+    _run_pair(dev, 2, 4, 3000, 2100, 4.0, 2)
+    print("[no-alloc] call without bias: B=8 H=16 M=1374 N=1369 (own-frame shape)", flush=True)
+    _run_pair(dev, 8, 16, 1374, 1369, 0.5, 3, with_bias=False)
+    print("[no-alloc] call without bias: B=3 H=16 M=1374 N=1369, smaller", flush=True)
+    _run_pair(dev, 3, 16, 1374, 1369, 2.0, 4, with_bias=False)
