@@ -107,6 +107,15 @@ template <bool F16> constexpr float kDown = F16 ? 1.0f : 96.0f;
 // per-tile maxima.  Other waves run the lazily moved offset from the start.
 template <bool F16> constexpr float kOptRange = F16 ? 20.0f : 260.0f;
 template <bool F16> constexpr float kOptOutlier = F16 ? 8.0f : 96.0f;
+// A wave that fails that test on tile 0 looks at the first kMainAhead tiles
+// (128 keys) instead and takes their max as x0 when their scores span at most
+// kOptRange4 and the outlier term stays within kOptOutlier4.  Calibrated on
+// N(0,1) q/k scaled up (68,700 keys, bias log counts): for fp16 the true max
+// then sits at most ~15.6 log2 units above the 128-key max at x12 (0 of 2,048
+// waves would overflow; all admitted), x14 admits 80 % of the waves of which
+// 0.9 % overflow and are recomputed, x16 admits none.
+template <bool F16> constexpr float kOptRange4 = F16 ? 34.0f : 320.0f;
+template <bool F16> constexpr float kOptOutlier4 = F16 ? 12.0f : 96.0f;
 constexpr int kRec = 36;                      // words per tile record
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -546,6 +555,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     mx = fmaxf(mx, x[15]);
     return max_halves(mx) * c;
   };
+  // Min over the row's live scores (keys past N score -inf), in log2 units.
+  auto row_min = [&](const f32x16& x) {
+    float mn = INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mn = x[r] > -INFINITY ? fminf(mn, x[r]) : mn;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mn), __float_as_uint(mn),
+                                                     false, false);
+    return fminf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+  };
   // P = 2^(S c - m) of one block in bf16, its row sums, then O += V^T . P.
   const __bf16 one = f32_to_half<F16>(1.0f);
   const bf16x4 ones4 = {one, one, one, one};
@@ -616,7 +634,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
     wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
     tile_barrier();
-    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    wait_tiles(std::integral_constant<int, 0>{});
     tile_barrier();
     auto carry = [&](const int t, MainTile& Tissue) {
       issue(t + kMainAhead, Tissue);
@@ -665,29 +683,56 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
   }
   // (Without the key maxima there is no bound to certify anything with.)
   fixed = !p.no_bound && __builtin_amdgcn_ballot_w64(bad) == 0;
+  float lo[kBlk], outl[kBlk];
   if (!fixed) {
     // The tile-0 offset, taken where tile 0's scores are narrow and no key
     // stands out (so that an overflow is unlikely); verified after the loop.
     bool wide = false;
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
-      float lo = INFINITY;                                 // min over the row's live scores
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lo = s_cur[j][r] > -INFINITY ? fminf(lo, s_cur[j][r]) : lo;
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(lo),
-                                                       false, false);
-      lo = fminf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
-      const float outl = __builtin_fmaf(q_norm[j], row_k - row_kmean, row_b - row_bmean);
+      lo[j] = row_min(s_cur[j]);
+      outl[j] = __builtin_fmaf(q_norm[j], row_k - row_kmean, row_b - row_bmean);
       wide = wide || !(x0s[j] > -INFINITY && x0s[j] < INFINITY) ||
-             !(x0s[j] - lo <= kOptRange<F16>) || !(outl <= kOptOutlier<F16>);
+             !(x0s[j] - lo[j] <= kOptRange<F16>) || !(outl[j] <= kOptOutlier<F16>);
     }
     opt = __builtin_amdgcn_ballot_w64(wide) == 0;
 #pragma unroll
     for (int j = 0; j < kBlk; ++j)
       m_off[j] = opt ? x0s[j] + kDown<F16> : kMInit;      // lazy: the first tile moves it
   }
-  wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+  // All kMainAhead tiles have landed past this barrier (every wave path waits
+  // for all of them here), so a wave may read any of them.
+  wait_tiles(std::integral_constant<int, 0>{});
   tile_barrier();
+  if (!fixed && !opt) {
+    // The tile-0 test failed: widen the sample to the first kMainAhead tiles
+    // (already in LDS; s_nxt is free until the loop) and take their row max
+    // as the offset if the scores seen so far are narrow enough (kOptRange4,
+    // kOptOutlier4); still verified after the loop.
+    float x4[kBlk];
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) x4[j] = x0s[j];
+#pragma unroll
+    for (int i = 1; i < kMainAhead; ++i)
+      if (i < ntiles) {
+        scores(*ring[i], s_nxt);
+#pragma unroll
+        for (int j = 0; j < kBlk; ++j) {
+          x4[j] = fmaxf(x4[j], row_max(s_nxt[j]));
+          lo[j] = fminf(lo[j], row_min(s_nxt[j]));
+        }
+      }
+    bool wide = false;
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j)
+      wide = wide || !(x4[j] > -INFINITY && x4[j] < INFINITY) ||
+             !(x4[j] - lo[j] <= kOptRange4<F16>) || !(outl[j] <= kOptOutlier4<F16>);
+    opt = __builtin_amdgcn_ballot_w64(wide) == 0;
+    if (opt) {
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) m_off[j] = x4[j] + kDown<F16>;
+    }
+  }
   }
 
   // Iteration t: refill the slot of tile t-1 with tile t+kMainAhead; S(t+1)
@@ -808,7 +853,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main_kernel(AttnArgs p) {
     for (int i = 0; i < kMainAhead; ++i) issue(i, *ring[i]);
     wait_tiles(std::integral_constant<int, kMainAhead - 1>{});
     tile_barrier();
-    wait_tiles(std::integral_constant<int, kMainAhead - 2>{});
+    wait_tiles(std::integral_constant<int, 0>{});
     tile_barrier();
     run(std::true_type{});
     wait_vm<0>();
