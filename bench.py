@@ -446,16 +446,19 @@ def main(argv=None) -> int:
             "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
             "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
         del qs, ks, vs, bs, out_a, lse_a, out_b, lse_b
-        # Row f2: the pooled shared set (kp 8: 25 seeds per frame) at 200 frames.
+        # Row f2: the pooled shared set at 200 frames: kp 8 (25 seeds per
+        # frame, seeds in registers) and kp 4 (100 seeds, super-chunks of 64).
         kk = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
         vv = (torch.randn(1, 16, S * P, 64, device=dev) / 8).bfloat16()
-        fn = lambda: torch.ops.gpa.pool_shared(kk, vv, S, pts, 37, 37, 8, False)  # noqa: E731
-        fn()
-        t = statistics.median(event_ms(fn, 5))
-        nbytes = 2 * 16 * S * (P - pts) * 64 * 2
-        kernels["pool_shared_200f_16h_kp8"] = {
-            "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
-            "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes}
+        for kp in (8, 4):
+            fn = lambda: torch.ops.gpa.pool_shared(kk, vv, S, pts, 37, 37, kp, False)  # noqa: E731
+            fn()
+            t = statistics.median(event_ms(fn, 5))
+            nbytes = 2 * 16 * S * (P - pts) * 64 * 2
+            kernels[f"pool_shared_200f_16h_kp{kp}"] = {
+                "ms": round(t, 4), "gbps": round(nbytes / (t * 1e-3) / 1e9, 1),
+                "pct_hbm": round(100 * nbytes / (t * 1e-3) / HBM_BYTES_PER_S, 2), "bytes": nbytes,
+                "seeds_per_frame": (-(-37 // kp)) ** 2}
         del kk, vv
         # Row f3: the merge front end (projection 1024 -> 128, normalise,
         # [dst | src] gather, bf16) on the fp32 norm1 output of 274,800 tokens.

@@ -97,6 +97,13 @@ void pool_shared_kernel(PoolArgs a) {
   const int npatch = a.gh * a.gw;
   const uint16_t* K = a.k + b * a.k_sb + h * a.k_sh + ((int64_t)s * a.P + a.pts) * a.k_sn;
   const uint16_t* Vp = a.v + b * a.v_sb + h * a.v_sh + ((int64_t)s * a.P + a.pts) * a.v_sn;
+  // The bases and output pointers, formed here so that the argument block's
+  // strides need not stay live in SGPRs (they spilled to VGPR lanes).
+  uint16_t* PK = a.pk;
+  uint16_t* PV = a.pv;
+  float* SZ = a.size;
+  int32_t* AS = a.assign;
+  asm volatile("" : "+s"(K), "+s"(Vp), "+s"(PK), "+s"(PV), "+s"(SZ), "+s"(AS));
 
   for (int g = tid; g < a.npool; g += kPoolThreads) count[g] = 0;
 
@@ -175,7 +182,7 @@ void pool_shared_kernel(PoolArgs a) {
       asg[p] = valid ? (uint8_t)bi : (uint8_t)0xff;   // 0xff matches no seed
       if (valid) {
         atomicAdd(&count[bi], 1);
-        if (a.assign) a.assign[(int64_t)grp * npatch + p] = bi;
+        if (AS) AS[(int64_t)grp * npatch + p] = bi;
       }
     }
   };
@@ -260,9 +267,226 @@ void pool_shared_kernel(PoolArgs a) {
     }
     reduce_store(acc, out);                    // the first barrier completes the counts
   };
-  sweep(K, a.k_sn, true, a.pk);
-  sweep(Vp, a.v_sn, false, a.pv);
-  for (int g = tid; g < a.npool; g += kPoolThreads) a.size[out_row0 + g] = (float)count[g];
+  sweep(K, a.k_sn, true, PK);
+  sweep(Vp, a.v_sn, false, PV);
+  for (int g = tid; g < a.npool; g += kPoolThreads) SZ[out_row0 + g] = (float)count[g];
+}
+
+// More than 64 seeds per frame (pool stride <= 4 at grid 37, down to every
+// patch a seed at stride 1): the seeds no longer fit in registers, so they
+// are taken in super-chunks of 64 (two blocks of 32, as above).
+//   Assignment: for each super-chunk every wave sweeps its tiles of K
+//   (tiles w, w+4, ...), scores them against the chunk's 64 normalised
+//   seeds exactly as above (16-bit rounded scores, lowest seed on ties) and
+//   keeps, per patch, the best score so far and its seed in LDS, replaced
+//   only by a strictly larger score of a later chunk: the same first maximum
+//   as one scan over all seeds in increasing order.  A patch whose scores
+//   are all NaN keeps seed 0, as above.
+//   Counts once the assignment is final, then the sums: per super-chunk, a
+//   sweep of K and one of V with the one-hot GEMM of the 64-seed kernel
+//   (seed ids now 16-bit), partial sums per wave over its tiles, the four
+//   waves added in wave order: every group mean is summed in the same order
+//   as in pool_shared_kernel.  K is read 2 * ceil(npool / 64) times and V
+//   ceil(npool / 64) times per frame (from L2 after the first sweep); one
+//   workgroup per (batch, head, frame) group as above.
+constexpr uint16_t kNoSeed = 0xffff;
+
+// The per-patch best scores (assignment) and the partial-sum buffer (sums)
+// share one LDS area: 68 KB in all, two workgroups per CU.
+constexpr int kManyUnion = kPoolWaves * kMaxPool * kRed > kMaxPatches
+                               ? kPoolWaves * kMaxPool * kRed : kMaxPatches;
+
+template <bool F16>
+__global__ __launch_bounds__(kPoolThreads) void pool_many_kernel(PoolArgs a) {
+  __shared__ int count[kMaxPatches];
+  __shared__ __attribute__((aligned(16))) uint16_t asg[kMaxPatches];
+  __shared__ __attribute__((aligned(16))) float area[kManyUnion];
+  __shared__ __attribute__((aligned(16))) uint16_t stage[kPoolWaves][32][kStage];
+  float* const best = area;                                              // assignment
+  float (*const red)[kMaxPool][kRed] = reinterpret_cast<float (*)[kMaxPool][kRed]>(area);  // sums
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int grp = blockIdx.x;                  // (b*H + h)*S + s
+  const int s = grp % a.S;
+  const int bh = grp / a.S;
+  const int h = bh % a.H, b = bh / a.H;
+  const int npatch = a.gh * a.gw;
+  const int ntile = (npatch + 31) / 32;        // ntile * 32 <= kMaxPatches
+  const int nsc = (a.npool + kMaxPool - 1) / kMaxPool;
+  const uint16_t* K = a.k + b * a.k_sb + h * a.k_sh + ((int64_t)s * a.P + a.pts) * a.k_sn;
+  const uint16_t* Vp = a.v + b * a.v_sb + h * a.v_sh + ((int64_t)s * a.P + a.pts) * a.v_sn;
+  const int64_t out_row0 = ((int64_t)bh * a.S + s) * a.npool;
+  uint16_t* PK = a.pk;
+  uint16_t* PV = a.pv;
+  float* SZ = a.size;
+  int32_t* AS = a.assign;
+  asm volatile("" : "+s"(K), "+s"(Vp), "+s"(PK), "+s"(PV), "+s"(SZ), "+s"(AS));
+
+  for (int g = tid; g < a.npool; g += kPoolThreads) count[g] = 0;
+  for (int p = tid; p < ntile * 32; p += kPoolThreads) {
+    asg[p] = kNoSeed;
+    best[p] = -INFINITY;
+  }
+
+  auto load_half = [&](const uint16_t* base, int64_t stride, int p, bf16x8 (&r)[4]) {
+    const uint16_t* row = base + (int64_t)p * stride + 8 * hi;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) r[ks] = *reinterpret_cast<const bf16x8*>(row + 16 * ks);
+  };
+  auto normalise = [&](const bf16x8 (&r)[4], bf16x8 (&nb)[4]) {
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = half_to_f32<F16>(r[ks][e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
+    const float inv = 1.0f / fmaxf(__builtin_sqrtf(sum_halves(ss)), 1e-6f);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nb[ks][e] = f32_to_half<F16>(half_to_f32<F16>(r[ks][e]) * inv);
+  };
+  __syncthreads();                             // counts and patch state cleared
+
+  // Assignment, one super-chunk of 64 seeds at a time.
+  for (int sc = 0; sc < nsc; ++sc) {
+    const int g0 = sc * kMaxPool;
+    bf16x8 seed[2][4];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int g = g0 + sb * 32 + l32;
+      const int gc = g < a.npool ? g : a.npool - 1;
+      const int gy = gc / a.nw, gx = gc % a.nw;
+      bf16x8 r[4];
+      load_half(K, a.k_sn, gy * a.kp * a.gw + gx * a.kp, r);
+      normalise(r, seed[sb]);
+      if (g >= a.npool)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) seed[sb][ks] = bf16x8{};
+    }
+    for (int t = wave; t < ntile; t += kPoolWaves) {
+      const int p = t * 32 + l32;
+      const bool valid = p < npatch;
+      bf16x8 rx[4], xb[4];
+      load_half(K, a.k_sn, valid ? p : npatch - 1, rx);
+      normalise(rx, xb);
+      float bv = -INFINITY;
+      int bi = g0;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        f32x16 sc16 = {};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) sc16 = mfma32x32x16_t<F16>(seed[sb][ks], xb[ks], sc16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {         // seeds in increasing order
+          const int g = g0 + sb * 32 + mfma_row(r, hi);
+          const float v = round16<F16>(sc16[r]);
+          if (g < a.npool && v > bv) {
+            bv = v;
+            bi = g;
+          }
+        }
+      }
+      const float pb = __shfl_xor(bv, 32);
+      const int pi = __shfl_xor(bi, 32);
+      if (pb > bv || (pb == bv && pi < bi)) {
+        bv = pb;
+        bi = pi;
+      }
+      // This wave owns tile t in every chunk, so its LDS updates are ordered.
+      if (hi == 0 && valid && bv > best[p]) {
+        best[p] = bv;
+        asg[p] = (uint16_t)bi;
+      }
+    }
+  }
+  __syncthreads();                             // assignment final; `best` is dead from here
+  for (int p = tid; p < npatch; p += kPoolThreads) {
+    uint16_t g = asg[p];
+    if (g == kNoSeed) {                        // every score NaN: seed 0
+      g = 0;
+      asg[p] = 0;
+    }
+    atomicAdd(&count[g], 1);
+    if (AS) AS[(int64_t)grp * npatch + p] = g;
+  }
+  __syncthreads();
+
+  uint16_t(&st)[32][kStage] = stage[wave];
+  // One-hot sums of a tile for the seeds g0 .. g0+63 (see sum_tile above).
+  auto sum_tile = [&](int t, int g0, bool valid, const bf16x8 (&rx)[4], f32x16 (&acc)[2][2]) {
+#pragma unroll
+    for (int fh = 0; fh < 2; ++fh) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<bf16x8*>(&st[l32][16 * c + 8 * hi]) = valid ? rx[2 * fh + c] : bf16x8{};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int r0 = 16 * kk + 8 * hi;       // rows r0 .. r0+7 of the tile
+        const u32x4 ab = *reinterpret_cast<const u32x4*>(&asg[t * 32 + r0]);
+        u32x4 bx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bx[q] = (uint32_t)st[r0 + 2 * q][l32] | ((uint32_t)st[r0 + 2 * q + 1][l32] << 16);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const uint32_t id = (uint32_t)(g0 + sb * 32 + l32);
+          u32x4 oh;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t b0 = ab[q] & 0xffffu, b1 = ab[q] >> 16;
+            oh[q] = (b0 == id ? kOne16<F16> : 0u) | (b1 == id ? kOne16<F16> << 16 : 0u);
+          }
+          acc[fh][sb] = mfma32x32x16_t<F16>(__builtin_bit_cast(bf16x8, oh),
+                                            __builtin_bit_cast(bf16x8, bx), acc[fh][sb]);
+        }
+      }
+    }
+  };
+  auto reduce_store = [&](f32x16 (&acc)[2][2], int g0, uint16_t* out) {
+    const int ng = min(kMaxPool, a.npool - g0);
+#pragma unroll
+    for (int fh = 0; fh < 2; ++fh) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave][sb * 32 + mfma_row(r, hi)][l32] = acc[fh][sb][r];
+      __syncthreads();
+      for (int e = tid; e < ng * 32; e += kPoolThreads) {
+        const int g = e >> 5, f = e & 31;
+        const float sum = ((red[0][g][f] + red[1][g][f]) + red[2][g][f]) + red[3][g][f];
+        const float inv = 1.0f / fmaxf((float)count[g0 + g], 1.0f);
+        out[(out_row0 + g0 + g) * kPoolD + 32 * fh + f] =
+            __builtin_bit_cast(uint16_t, f32_to_half<F16>(sum * inv));
+      }
+      __syncthreads();
+    }
+  };
+  auto sweep = [&](const uint16_t* X, int64_t x_sn, int g0, uint16_t* out) {
+    f32x16 acc[2][2] = {};
+    bf16x8 nx[4];
+    const int p0 = wave * 32 + l32;
+    load_half(X, x_sn, p0 < npatch ? p0 : npatch - 1, nx);
+    for (int t = wave; t < ntile; t += kPoolWaves) {
+      const int p = t * 32 + l32;
+      const bool valid = p < npatch;
+      bf16x8 rx[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) rx[ks] = nx[ks];
+      const int pn = p + 32 * kPoolWaves;
+      load_half(X, x_sn, pn < npatch ? pn : npatch - 1, nx);
+      sum_tile(t, g0, valid, rx, acc);
+    }
+    reduce_store(acc, g0, out);
+  };
+  for (int sc = 0; sc < nsc; ++sc) {
+    sweep(K, a.k_sn, sc * kMaxPool, PK);
+    sweep(Vp, a.v_sn, sc * kMaxPool, PV);
+  }
+  for (int g = tid; g < a.npool; g += kPoolThreads) SZ[out_row0 + g] = (float)count[g];
 }
 
 }  // namespace
@@ -301,9 +525,9 @@ int pool_run(const char* fn, const void* k, const void* v, void* pooled_k, void*
     return GPA_E_INVALID;
   }
   const int64_t nh = (grid_h + kp - 1) / kp, nw = (grid_w + kp - 1) / kp;
-  if (nh * nw > kMaxPool || grid_h * grid_w > kMaxPatches) {
-    gpa_set_error("%s: %lld seeds / %lld patches exceed the kernel's 64 / 4096", fn,
-                  (long long)(nh * nw), (long long)(grid_h * grid_w));
+  if (grid_h * grid_w > kMaxPatches) {
+    gpa_set_error("%s: %lld patches exceed the kernel's 4096", fn,
+                  (long long)(grid_h * grid_w));
     return GPA_E_UNSUPPORTED;
   }
   const bool aligned = (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 &&
@@ -332,7 +556,10 @@ int pool_run(const char* fn, const void* k, const void* v, void* pooled_k, void*
   a.H = (int)H; a.S = (int)S; a.P = (int)P; a.pts = (int)pts;
   a.gh = (int)grid_h; a.gw = (int)grid_w;
   a.kp = (int)kp; a.nw = (int)nw; a.npool = (int)(nh * nw);
-  if (a.npool > 32)
+  if (a.npool > kMaxPool)
+    hipLaunchKernelGGL((pool_many_kernel<F16>), dim3((unsigned)groups), dim3(kPoolThreads), 0,
+                       (hipStream_t)stream, a);
+  else if (a.npool > 32)
     hipLaunchKernelGGL((pool_shared_kernel<2, F16>), dim3((unsigned)groups), dim3(kPoolThreads), 0,
                        (hipStream_t)stream, a);
   else

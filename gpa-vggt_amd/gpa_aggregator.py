@@ -333,20 +333,21 @@ class GpaAttention(nn.Module):
         return combine_by_lse(out_a, lse_a, out_b, lse_b, S)
 
 
-POOL_KERNEL_MAX_SEEDS = 64      # seeds per frame the gpa::pool_shared kernel holds
+POOL_KERNEL_MAX_PATCHES = 4096   # patches per frame the gpa::pool_shared kernels hold
 
 
 def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, grid_h: int,
                     grid_w: int, kp: int, want_assign: bool = False):
     """The pooled summaries of the shared set (attention.py:113-140) from
     k, v [B, H, S*P, D] on a grid_h x grid_w patch grid (ph x pw there): the
-    `gpa::pool_shared` kernel for up to 64 seeds per frame (pool stride >= 5
-    at grid 37, the reference default 8 included); above that (stride <= 4)
-    the reference's own torch ops on the device (`pool_shared_torch`).
+    `gpa::pool_shared` kernels for bf16/fp16 k and v of head dim 64 and up
+    to 4,096 patches per frame, any pool stride (seeds held in registers up
+    to 64 per frame, in super-chunks of 64 above); otherwise the
+    reference's own torch ops on the device (`pool_shared_torch`).
     Returns (pooled_k, pooled_v [B, H, S*npool, D], size [B, H, S, npool]
     fp32, assign [B, H, S, grid_h*grid_w] or an empty tensor)."""
-    npool = -(-grid_h // kp) * -(-grid_w // kp)
-    if npool <= POOL_KERNEL_MAX_SEEDS and k.dtype in (torch.bfloat16, torch.float16):
+    if (grid_h * grid_w <= POOL_KERNEL_MAX_PATCHES and k.shape[-1] == 64
+            and k.dtype in (torch.bfloat16, torch.float16)):
         return torch.ops.gpa.pool_shared(k, v, frames, pts, grid_h, grid_w, kp, want_assign)
     B, H, N, D = k.shape
     P = N // frames
@@ -358,9 +359,9 @@ def pool_shared_set(k: torch.Tensor, v: torch.Tensor, frames: int, pts: int, gri
 def pool_shared_torch(k5: torch.Tensor, v5: torch.Tensor, pts: int, grid_h: int, grid_w: int,
                       kp: int):
     """Content-adaptive pooled summaries of the shared K/V set (attention.py:113-140),
-    restated with torch ops.  The harness runs the `gpa::pool_shared` kernel
-    up to 64 seeds per frame and this restatement above that (pool stride
-    <= 4 at grid 37); the tests pin the kernel against it.
+    restated with torch ops.  The harness runs the `gpa::pool_shared`
+    kernels wherever they apply (bf16/fp16, head dim 64, <= 4,096 patches)
+    and this restatement otherwise; the tests pin the kernels against it.
 
     k5/v5 [B, H, S, P, D], patches row-major on a grid_h x grid_w grid.
     Seeds are the stride-kp lattice patches; every patch joins the seed whose

@@ -301,7 +301,7 @@ int gpa_qk_norm_rope_f16(const void* qkv, int64_t B, int64_t N, int64_t H, int64
  * (p < grid_h*grid_w on a grid_h-row, grid_w-column patch grid, row-major;
  * D = 64):
  *   seeds y_g: the patches (gy*kp, gx*kp), g = gy*nw + gx, nh = ceil(grid_h/kp),
- *              nw = ceil(grid_w/kp), npool = nh*nw (<= 64)
+ *              nw = ceil(grid_w/kp), npool = nh*nw (any kp >= 1)
  *   assign a_p = argmax_g bf16(bf16(x_p/max(|x_p|,1e-6)) . bf16(y_g/max(|y_g|,1e-6)))
  *              (fp32 dots rounded to bf16; the lowest g wins ties)
  *   size[b,h,s,g]         = #{p : a_p = g}                                (fp32)
@@ -309,8 +309,10 @@ int gpa_qk_norm_rope_f16(const void* qkv, int64_t B, int64_t N, int64_t H, int64
  *   pooled_v likewise from v (same token positions).
  * pooled_k / pooled_v are contiguous [B, H, S*npool, 64], size [B, H, S, npool];
  * assign (nullable) receives a_p as int32 [B, H, S, grid_h*grid_w].  k and v
- * rows 16-byte aligned, unit feature stride; grid_h*grid_w <= 4096.  More
- * than 64 seeds: GPA_E_UNSUPPORTED.  The sums run in fp32 in a fixed order,
+ * rows 16-byte aligned, unit feature stride; grid_h*grid_w <= 4096 (else
+ * GPA_E_UNSUPPORTED).  Up to 64 seeds per frame they stay in registers;
+ * above, they are scored and summed in super-chunks of 64 (K read twice and
+ * V once per chunk).  The sums run in fp32 in a fixed order,
  * so the means are deterministic (the reference's scatter_add_ sums with
  * atomics in a run-dependent order).
  * Replaces `_pool` of vggt/layers/attention.py:113-140 (ph = grid_h,

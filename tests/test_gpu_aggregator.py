@@ -147,10 +147,10 @@ def test_merged_block_attention_matches_reference(dev, gh, gw):
                                       (-1, 37, 37), (8, 28, 37), (4, 28, 37), (5, 37, 28)])
 def test_frame_special_block_attention_matches_reference(dev, kp, gh, gw):
     """The frame-special block for the pool strides the reference accepts
-    (attention.py:106-108, 178-190): kp > 0 pooled summaries (the kernel up
-    to 64 seeds, e.g. kp 8 and 5 at 37 x 37; the torch restatement above,
-    kp 4), kp = 0 the special tokens only, kp < 0 plain frame attention; on
-    square and rectangular patch grids (ph x pw = gh x gw)."""
+    (attention.py:106-108, 178-190): kp > 0 pooled summaries (the pooling
+    kernel: 25, 64 and, in super-chunks of 64, 100 seeds at kp 8, 5 and 4 on
+    37 x 37), kp = 0 the special tokens only, kp < 0 plain frame attention;
+    on square and rectangular patch grids (ph x pw = gh x gw)."""
     cfg, blk = _block(dev, seed=1, gh=gh, gw=gw)
     cfg.broadcast_pool = kp
     blk.attn.frame_special = True
@@ -309,15 +309,19 @@ def _pool_bf16_fp64(x: torch.Tensor, gh: int, gw: int, kp: int):
     (37, 37, 8), (37, 37, 5),     # the 518 x 518 grid: 25 and 64 seeds
     (28, 37, 8), (37, 28, 5),     # 392 x 518 and 518 x 392 images: 20 and 48 seeds
     (13, 50, 7),                  # ragged last tile and lattice row
-    (64, 64, 8),                  # 4096 patches, 64 seeds: the kernel's limits
+    (64, 64, 8),                  # 4096 patches (the kernel's limit), 64 seeds
     (1, 1, 8),                    # one patch, one seed
+    (37, 37, 4), (28, 37, 3),     # more than 64 seeds: 100 and 130 (super-chunks of 64)
+    (37, 37, 2), (37, 37, 1),     # 361 seeds; every patch a seed (1,369)
+    (64, 64, 2),                  # 4096 patches, 1,024 seeds
 ])
 def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     """gpa::pool_shared against the scores in fp64 (assignment, except rows
     whose best two scores are within two bf16 steps, where the bf16 rounding
     of the reference's scores decides) and, given its own assignment, exact
     sizes and fp64 means of the K and V rows; bit-identical on a second call
-    and on strided V rows.  Square and rectangular patch grids."""
+    and on strided V rows.  Square and rectangular patch grids, every pool
+    stride the reference accepts down to 1 (attention.py:106-140)."""
     g = torch.Generator(device=dev).manual_seed(gh * 100 + gw + kp)
     B, H, S = 1, 4, 3
     P_ = PTS + gh * gw
@@ -364,7 +368,7 @@ def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     assert torch.equal(pk3, pk) and torch.equal(pv3, pv)
 
 
-@pytest.mark.parametrize("gh,gw,kp", [(37, 37, 8), (28, 37, 5)])
+@pytest.mark.parametrize("gh,gw,kp", [(37, 37, 8), (28, 37, 5), (37, 37, 3)])
 def test_pool_shared_kernel_fp16(dev, gh, gw, kp):
     """The fp16 instantiation (the pooling under fp16 autocast): assignment
     equal to the fp64 argmax over fp16-rounded normalised rows wherever the

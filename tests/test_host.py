@@ -251,8 +251,6 @@ def _pool(**kw):
     (dict(k=None), _native.GPA_E_INVALID),
     (dict(size=None), _native.GPA_E_INVALID),
     (dict(P=1000), _native.GPA_E_INVALID),                  # frame too short for the grid
-    (dict(kp=4), _native.GPA_E_UNSUPPORTED),                # 100 seeds > 64
-    (dict(gh=28, kp=4), _native.GPA_E_UNSUPPORTED),         # 7 x 10 = 70 seeds > 64
     (dict(gh=65, gw=64, P=4165, kp=9), _native.GPA_E_UNSUPPORTED),  # 4160 patches > 4096
     (dict(gh=-1), _native.GPA_E_INVALID),
     (dict(gw=38), _native.GPA_E_INVALID),                   # 37 x 38 patches + 5 > P
