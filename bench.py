@@ -504,6 +504,18 @@ def main(argv=None) -> int:
         kernels["sim_argmax_200f_207955x66845x1024"] = kernel_entry(
             W.sim_flops(1, 207_955, 66_845, 1024), t)
         del s3, d3
+        # Head dims other than 64 (the reference kernel's HEAD_DIM is a
+        # template constant): 128, 16 heads x 65,536 queries x 68,700 keys.
+        qd = (torch.randn(1, 16, 65_536, 128, device=dev) / 8).bfloat16()
+        kd = (torch.randn(1, 16, 68_700, 128, device=dev) / 8).bfloat16()
+        vd = (torch.randn(1, 16, 68_700, 128, device=dev) / 8).bfloat16()
+        bd = bias[..., :68_700]
+        fn = lambda: attention_keybias(qd, kd, vd, bd, 128 ** -0.5)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 3))
+        kernels["attn_keybias_d128_16h_65536x68700"] = kernel_entry(
+            W.attn_flops(16, 65_536, 68_700, 128), t)
+        del qd, kd, vd, bd
         log("[bench] 200-frame shapes done")
 
     if not args.no_200f:

@@ -71,6 +71,8 @@
 #include <math.h>
 
 #include <mutex>
+
+#include "attn_any_dim.h"
 #include <type_traits>
 
 namespace gpa {
@@ -975,8 +977,8 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
     gpa_set_error("%s: empty key set (N=0)", fn);
     return GPA_E_INVALID;
   }
-  if (D != kHD) {
-    gpa_set_error("%s: head_dim %lld unsupported (only 64)", fn, (long long)D);
+  if (D != kHD && !attn_any_dim_supported(D)) {
+    gpa_set_error("%s: head_dim %lld unsupported (16, 32, 64, 128 or 256)", fn, (long long)D);
     return GPA_E_UNSUPPORTED;
   }
   if (!q || !k || !v || !o) {
@@ -1037,6 +1039,35 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   hipStream_t s = (hipStream_t)stream;
   const int64_t ntiles = (N + kKT - 1) / kKT;
   const float c = sm_scale * kLog2e;
+  if (D != kHD) {
+    // Head dims other than 64: the running-max kernel, no pre-passes (the
+    // workspace goes unused).
+    AnyDimArgs g{};
+    g.q = (const uint16_t*)q;
+    g.k = (const uint16_t*)k;
+    g.v = (const uint16_t*)v;
+    g.bias = bias;
+    g.o = (uint16_t*)o;
+    g.lse = lse;
+    g.H = (int)H;
+    g.BH = B * H;
+    g.M = M;
+    g.N = N;
+    g.q_sb = q_sb; g.q_sh = q_sh; g.q_sm = q_sm;
+    g.k_sb = k_sb; g.k_sh = k_sh; g.k_sn = k_sn;
+    g.v_sb = v_sb; g.v_sh = v_sh; g.v_sn = v_sn;
+    g.o_sb = o_sb; g.o_sh = o_sh; g.o_sm = o_sm;
+    g.bias_sb = bias_sb; g.bias_sh = bias_sh; g.bias_sn = bias_sn;
+    g.lse_sb = lse_sb; g.lse_sh = lse_sh;
+    g.c = c;
+    g.mul = 1.0f / sm_scale;
+    const hipError_t ge = attn_any_dim_launch<F16>(g, D, bias_kind, s);
+    if (ge != hipSuccess) {
+      gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(ge));
+      return GPA_E_LAUNCH;
+    }
+    return GPA_OK;
+  }
 
   RecArgs ra{};
   ra.k = (const uint16_t*)k;

@@ -112,7 +112,9 @@ def _attn(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(H=-1), _native.GPA_E_INVALID),
     (dict(N=0), _native.GPA_E_INVALID),
-    (dict(D=128), _native.GPA_E_UNSUPPORTED),
+    (dict(D=48), _native.GPA_E_UNSUPPORTED),                # not a power of two
+    (dict(D=512, qsm=512, ksn=512, vsn=512, osm=512), _native.GPA_E_UNSUPPORTED),
+    (dict(D=8), _native.GPA_E_UNSUPPORTED),
     (dict(q=None), _native.GPA_E_INVALID),
     (dict(bias_kind=7), _native.GPA_E_INVALID),
     (dict(bias_kind=1), _native.GPA_E_INVALID),      # bias kind without a pointer
