@@ -20,6 +20,10 @@
   merge  deterministic K/V merge, [1,16,274800,64] fp32 rows into 66,845 slots
   front  merge front end: 274,800 fp32 metric rows of 1024 -> bf16 [dst | src] x 128
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
+  pool4  the same at pool stride 4: 100 seeds per frame, the super-chunked
+         kernel (not in `all`)
+  attn128 attention at head dim 128: 16 heads x 65,536 queries x 68,700 keys,
+         log-count bias (the running-max kernel; not in `all`)
   qk     qk LayerNorm + 2D RoPE of a 200-frame block: the bf16 QKV projection
          [1, 274800, 3072] to bf16 q and k, then to bf16 q and fp32 k
   combine LSE combine of the frame-special split at 200 frames (bf16)
@@ -54,7 +58,8 @@ def main(argv=None) -> int:
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
     if which not in ("sim", "sim200", "sim1024", "attn", "sharp", "own", "shared", "merge", "front",
-                     "pool", "qk", "combine", "sim16", "attn16", "attn0", "copy", "all"):
+                     "pool", "pool4", "attn128", "qk", "combine", "sim16", "attn16", "attn0",
+                     "copy", "all"):
         print(__doc__, file=sys.stderr)
         return 2
 
@@ -129,6 +134,22 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"pool 16x200 frames kp 8 x {reps} done", flush=True)
         del kk, vv
+    if which == "pool4":
+        kk = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        vv = (torch.randn(1, 16, 200 * 1374, 64, device=dev) / 8).bfloat16()
+        for _ in range(reps):
+            torch.ops.gpa.pool_shared(kk, vv, 200, 5, 37, 37, 4, False)
+        torch.cuda.synchronize()
+        print(f"pool4 16x200 frames kp 4 (100 seeds) x {reps} done", flush=True)
+        del kk, vv
+    if which == "attn128":
+        q, k, v, b = W.attn_inputs(m=274_800, n=68_700, d=128, device=dev)
+        q = q[:, :, :65_536].contiguous()
+        for _ in range(reps):
+            attention_keybias(q, k, v, b, 128 ** -0.5)
+        torch.cuda.synchronize()
+        print(f"attn128 16x65536x68700x128 x {reps} done", flush=True)
+        del q, k, v, b
     if which in ("qk", "all"):
         import gpa_aggregator as A
         qkv = torch.randn(1, 200 * 1374, 3 * 1024, device=dev).bfloat16()
