@@ -21,10 +21,17 @@ struct AnyDimArgs {
   int64_t lse_sb, lse_sh;
   float c;                // sm_scale * log2(e)
   float mul;              // 1 / sm_scale
+  float* ws;              // workspace (the bias rows of head dims 128 and 256)
+  size_t ws_bytes;
 };
 
-// Head dims the kernel is built for: 16, 32, 128, 256.
+// Head dims the kernels are built for: 16, 32, 128, 256.
 bool attn_any_dim_supported(int64_t D);
+
+// Workspace bytes a call at head dim D needs (the fp32 bias rows of the
+// tiled kernel: B*H rows of N rounded up to 32 keys); at most the head-dim-64
+// workspace of the same shape.
+size_t attn_any_dim_ws_bytes(int64_t BH, int64_t N, int64_t D);
 
 // Launch on `s`; returns hipGetLastError() of the launch.
 template <bool F16>

@@ -1040,8 +1040,19 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
   const int64_t ntiles = (N + kKT - 1) / kKT;
   const float c = sm_scale * kLog2e;
   if (D != kHD) {
-    // Head dims other than 64: the running-max kernel, no pre-passes (the
-    // workspace goes unused).
+    // Head dims other than 64 (attn_any_dim.hip): 16 and 32 run the
+    // running-max kernel without pre-passes, 128 and 256 the tiled kernel,
+    // whose bias rows (4 bytes per key) fit in the records' place (144 bytes
+    // per 32 keys).
+    if (((M + 127) / 128) * B * H > 0xffffffffLL) {   // 128-query workgroups, 32-bit numbering
+      gpa_set_error("%s: %lld query blocks exceed the grid limit", fn,
+                    (long long)(((M + 127) / 128) * B * H));
+      return GPA_E_UNSUPPORTED;
+    }
+    if (attn_any_dim_ws_bytes(B * H, N, D) > rec_bytes(B, H, N)) {
+      gpa_set_error("%s: internal: bias rows exceed the workspace", fn);
+      return GPA_E_WORKSPACE;
+    }
     AnyDimArgs g{};
     g.q = (const uint16_t*)q;
     g.k = (const uint16_t*)k;
@@ -1061,6 +1072,8 @@ int attn_keybias_run(const char* fn, const void* q, const void* k, const void* v
     g.lse_sb = lse_sb; g.lse_sh = lse_sh;
     g.c = c;
     g.mul = 1.0f / sm_scale;
+    g.ws = (float*)workspace;
+    g.ws_bytes = workspace_bytes;
     const hipError_t ge = attn_any_dim_launch<F16>(g, D, bias_kind, s);
     if (ge != hipSuccess) {
       gpa_set_error("%s: launch failed: %s", fn, hipGetErrorString(ge));

@@ -102,3 +102,25 @@ def test_head_dim_fp32_inputs_follow_the_cast_contract(dev):
                             b.to(dev).bfloat16(), 32 ** -0.5)
     assert o32.dtype == torch.bfloat16
     assert torch.equal(o32, o16)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rise", [20.0, 90.0])
+def test_late_key_moves_the_offset(dev, D, dtype, rise):
+    """Head dims 128 and 256 keep a softmax offset that moves only when a
+    tile's row max rises more than 15 (fp16 P) or 64 (bf16 P) log2 units
+    above it.  A key in the last tile aligned with every query lifts the row
+    max ~`rise` log2 units above the earlier tiles, so the offset moves on a
+    late tile (for fp16 at both rises, for bf16 at 90) and the output
+    accumulated so far is rescaled; rows then concentrate on that key."""
+    B, H, M, N = 1, 2, 256, 1000
+    q, k, v, b = _inputs(B, H, M, N, D, seed=int(rise) + D, dtype=torch.float32, bias="f32")
+    g = torch.Generator().manual_seed(D)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = q + 2.0 * u                                   # every query has q.u ~ 2
+    alpha = rise * D ** 0.5 / (2.0 * math.log2(math.e))
+    k[:, :, N - 7] = alpha * u                        # score ~ rise log2 units
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    _check(dev, q, k, v, b, D, tight=False)
