@@ -515,6 +515,16 @@ def main(argv=None) -> int:
         t = statistics.median(event_ms(fn, 3))
         kernels["attn_keybias_d128_16h_65536x68700"] = kernel_entry(
             W.attn_flops(16, 65_536, 68_700, 128), t)
+        del qd, kd, vd
+        # ... and 256, 16 heads x 32,768 queries (the same FLOP count).
+        qd = (torch.randn(1, 16, 32_768, 256, device=dev) / 8).bfloat16()
+        kd = (torch.randn(1, 16, 68_700, 256, device=dev) / 8).bfloat16()
+        vd = (torch.randn(1, 16, 68_700, 256, device=dev) / 8).bfloat16()
+        fn = lambda: attention_keybias(qd, kd, vd, bd, 256 ** -0.5)  # noqa: E731
+        fn()
+        t = statistics.median(event_ms(fn, 3))
+        kernels["attn_keybias_d256_16h_32768x68700"] = kernel_entry(
+            W.attn_flops(16, 32_768, 68_700, 256), t)
         del qd, kd, vd, bd
         log("[bench] 200-frame shapes done")
 
