@@ -23,7 +23,7 @@
   pool4  the same at pool stride 4: 100 seeds per frame, the super-chunked
          kernel (not in `all`)
   attn128 attention at head dim 128: 16 heads x 65,536 queries x 68,700 keys,
-         log-count bias (the running-max kernel; not in `all`)
+         log-count bias (the tiled kernel; not in `all`)
   qk     qk LayerNorm + 2D RoPE of a 200-frame block: the bf16 QKV projection
          [1, 274800, 3072] to bf16 q and k, then to bf16 q and fp32 k
   combine LSE combine of the frame-special split at 200 frames (bf16)

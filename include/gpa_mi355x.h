@@ -125,14 +125,17 @@ int gpa_sim_argmax_f16(const void* a, const void* b,
  * (padded past N) and two per-tile maxima the kernel bounds its scores with,
  * 16 bytes of row maxima and means, and one flag byte per 64 queries.  The
  * reference wrapper allocates the analogous padded bias buffer
- * (merging/fused_attention.py:159-160). */
+ * (merging/fused_attention.py:159-160).  At head dims 128 and 256 the call
+ * writes one fp32 bias row per (batch, head) there instead (4 bytes per key,
+ * rounded up to 32 keys), which the same size holds. */
 size_t gpa_attn_keybias_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t N);
 
 /*
  * Attention with a per-key additive bias, head_dim D in {16, 32, 64, 128,
  * 256} (the reference kernel's HEAD_DIM, fused_attention.py:82, 97, 177).
  * D = 64 (VGGT) runs the tuned kernel with a certified fixed softmax
- * offset; the other head dims a running-max kernel with the same contract.
+ * offset; D = 128 and 256 a tiled kernel with a lazily moved offset, D = 16
+ * and 32 a running-max kernel, all with the same contract.
  *   o[b,h,m,:] = softmax_n( q[b,h,m,:].k[b,h,n,:] * sm_scale + bias[b,h,n] ) . v[b,h,n,:]
  *   lse[b,h,m] = log2( sum_n 2^( (q.k*sm_scale + bias) * log2(e) ) )   (if lse != NULL)
  * Replaces merging/fused_attention.py:130-180 (`attention_keybias`) and the
