@@ -425,6 +425,27 @@ def main(argv=None) -> int:
         out_a, lse_a = fn()
         t = statistics.median(event_ms(fn, 5))
         kernels["attn_frame_own_3200bh_1374x1369"] = kernel_entry(W.attn_flops(S * 16, P, P - pts, 64), t)
+        # The same call on torch's own fused kernels (no bias, so flash and
+        # memory-efficient SDPA apply; outputs only, no LSE): the floor a
+        # caller without this library would get at the frame shape.
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        own_floor = {}
+        for be, tag in ((SDPBackend.FLASH_ATTENTION, "flash"),
+                        (SDPBackend.EFFICIENT_ATTENTION, "efficient")):
+            def sdpa_own(be=be):
+                with sdpa_kernel([be]):
+                    return torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, scale=SM_SCALE)
+            try:
+                sdpa_own()
+                ts = statistics.median(event_ms(sdpa_own, 5))
+                ent = kernel_entry(W.attn_flops(S * 16, P, P - pts, 64), ts)
+                ent["this_kernel_speedup"] = round(ts / t, 3)
+                ent["backend"] = str(be)
+                own_floor[f"torch_sdpa_unmasked_{tag}"] = ent
+                log(f"[bench] own-frame shape, torch SDPA {tag}: {ts:.3f} ms")
+            except RuntimeError as e:
+                own_floor[f"torch_sdpa_unmasked_{tag}"] = {"error": str(e).splitlines()[0][:200]}
+        kernels["attn_frame_own_3200bh_1374x1369"]["floor"] = own_floor
         del kf, vf
         qs = qf.view(1, S, 16, P, 64).permute(0, 2, 1, 3, 4).reshape(1, 16, S * P, 64)
         del qf
