@@ -3,9 +3,10 @@ reference kernel takes HEAD_DIM as a constexpr and its wrapper reads it
 from q (merging/fused_attention.py:82, 89, 97, 146, 177).  Checked against
 the fp32 oracle on the same 16-bit inputs, output and log2 LSE, for both
 operand formats, every bias kind, ragged query and key counts (partial
-tiles, one key), sharp logits, strided views and the allocation-free entry
-point; head dim 64 keeps the tuned kernel, so a 64-d slice of the same data
-must agree with the oracle to the same bar.
+tiles, one key), sharp logits, a late key that moves the softmax offset of
+the tiled kernel, and strided views (the allocation-free entry point at head
+dim 128: test_zz_no_alloc.py); head dim 64 keeps the tuned kernel, so a
+64-d slice of the same data must agree with the oracle to the same bar.
 
 Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 on unit-scale values; the LSE
 within 2^-8 / ln 2 (the 16-bit P of the P.V product is not in the row sum
