@@ -69,8 +69,9 @@ def test_head_dims_match_oracle(dev, D, dtype, B, H, M, N, bias):
 
 @pytest.mark.parametrize("D", [32, 128])
 def test_head_dims_sharp_logits(dev, D):
-    """Logits spread over ~100 log2 units: the running max moves on late
-    tiles and the rescale path carries the result."""
+    """Logits spread over ~100 log2 units: the running max (16, 32) or the
+    lazily moved offset (128) moves on late tiles and the rescale path
+    carries the result."""
     q, k, v, b = _inputs(1, 2, 400, 2000, D, seed=5, dtype=torch.bfloat16, qk_scale=3.0)
     _check(dev, q, k, v, b, D)
 
