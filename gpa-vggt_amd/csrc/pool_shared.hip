@@ -290,6 +290,10 @@ void pool_shared_kernel(PoolArgs a) {
 //   ceil(npool / 64) times per frame (from L2 after the first sweep); one
 //   workgroup per (batch, head, frame) group as above.
 constexpr uint16_t kNoSeed = 0xffff;
+// Tiles per wave in flight in the many-seed sweeps (each sweep is a chain of
+// short per-tile steps; with one tile ahead it waited out most of each
+// tile's load).
+constexpr int kManyAhead = 2;
 
 // The per-patch best scores (assignment) and the partial-sum buffer (sums)
 // share one LDS area: 68 KB in all, two workgroups per CU.
@@ -297,7 +301,7 @@ constexpr int kManyUnion = kPoolWaves * kMaxPool * kRed > kMaxPatches
                                ? kPoolWaves * kMaxPool * kRed : kMaxPatches;
 
 template <bool F16>
-__global__ __launch_bounds__(kPoolThreads) void pool_many_kernel(PoolArgs a) {
+__global__ __launch_bounds__(kPoolThreads, 2) void pool_many_kernel(PoolArgs a) {
   __shared__ int count[kMaxPatches];
   __shared__ __attribute__((aligned(16))) uint16_t asg[kMaxPatches];
   __shared__ __attribute__((aligned(16))) float area[kManyUnion];
@@ -367,11 +371,22 @@ __global__ __launch_bounds__(kPoolThreads) void pool_many_kernel(PoolArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) seed[sb][ks] = bf16x8{};
     }
-    for (int t = wave; t < ntile; t += kPoolWaves) {
+    // This wave's next two tiles in registers (one slot per unrolled step),
+    // so two tiles' loads are in flight while one is scored.
+    bf16x8 ring[kManyAhead][4];
+#pragma unroll
+    for (int j = 0; j < kManyAhead; ++j) {
+      const int pj = (wave + kPoolWaves * j) * 32 + l32;
+      load_half(K, a.k_sn, pj < npatch ? pj : npatch - 1, ring[j]);
+    }
+    auto assign_tile = [&](const int t, bf16x8 (&slot)[4]) {
       const int p = t * 32 + l32;
       const bool valid = p < npatch;
       bf16x8 rx[4], xb[4];
-      load_half(K, a.k_sn, valid ? p : npatch - 1, rx);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) rx[ks] = slot[ks];
+      const int pn = p + 32 * kPoolWaves * kManyAhead;
+      load_half(K, a.k_sn, pn < npatch ? pn : npatch - 1, slot);
       normalise(rx, xb);
       float bv = -INFINITY;
       int bi = g0;
@@ -401,6 +416,12 @@ __global__ __launch_bounds__(kPoolThreads) void pool_many_kernel(PoolArgs a) {
         best[p] = bv;
         asg[p] = (uint16_t)bi;
       }
+    };
+    static_assert(kManyAhead == 2, "the loop below is unrolled over two slots");
+    for (int t = wave; t < ntile; t += kPoolWaves * kManyAhead) {
+      assign_tile(t, ring[0]);
+      if (t + kPoolWaves >= ntile) break;
+      assign_tile(t + kPoolWaves, ring[1]);
     }
   }
   __syncthreads();                             // assignment final; `best` is dead from here
@@ -467,18 +488,26 @@ __global__ __launch_bounds__(kPoolThreads) void pool_many_kernel(PoolArgs a) {
   };
   auto sweep = [&](const uint16_t* X, int64_t x_sn, int g0, uint16_t* out) {
     f32x16 acc[2][2] = {};
-    bf16x8 nx[4];
-    const int p0 = wave * 32 + l32;
-    load_half(X, x_sn, p0 < npatch ? p0 : npatch - 1, nx);
-    for (int t = wave; t < ntile; t += kPoolWaves) {
+    bf16x8 ring[kManyAhead][4];
+#pragma unroll
+    for (int j = 0; j < kManyAhead; ++j) {
+      const int pj = (wave + kPoolWaves * j) * 32 + l32;
+      load_half(X, x_sn, pj < npatch ? pj : npatch - 1, ring[j]);
+    }
+    auto step = [&](const int t, bf16x8 (&slot)[4]) {
       const int p = t * 32 + l32;
       const bool valid = p < npatch;
       bf16x8 rx[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) rx[ks] = nx[ks];
-      const int pn = p + 32 * kPoolWaves;
-      load_half(X, x_sn, pn < npatch ? pn : npatch - 1, nx);
+      for (int ks = 0; ks < 4; ++ks) rx[ks] = slot[ks];
+      const int pn = p + 32 * kPoolWaves * kManyAhead;
+      load_half(X, x_sn, pn < npatch ? pn : npatch - 1, slot);
       sum_tile(t, g0, valid, rx, acc);
+    };
+    for (int t = wave; t < ntile; t += kPoolWaves * kManyAhead) {
+      step(t, ring[0]);
+      if (t + kPoolWaves >= ntile) break;
+      step(t + kPoolWaves, ring[1]);
     }
     reduce_store(acc, g0, out);
   };
