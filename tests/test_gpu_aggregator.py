@@ -368,6 +368,44 @@ def test_pool_shared_kernel_matches_reference(dev, gh, gw, kp):
     assert torch.equal(pk3, pk) and torch.equal(pv3, pv)
 
 
+@pytest.mark.parametrize("gh,gw,kp", [(37, 37, 8), (37, 37, 4), (37, 37, 1)])
+def test_pool_shared_kernel_empty_seeds(dev, gh, gw, kp):
+    """Seeds whose key equals an earlier seed's tie with it on every patch,
+    and the lowest seed wins (`argmax`'s first maximum), so they end with no
+    members: size 0 and a zero summary (the count clamp).  Seeds 1-3 of
+    every frame are copies of seed 0's key; the other groups keep their fp64
+    means over the kernel's own assignment, and a second call is
+    bit-identical (both the 64-seed kernel and the sorted member lists of
+    the many-seed kernel)."""
+    g = torch.Generator(device=dev).manual_seed(gh + gw + 10 * kp)
+    B, H, S = 1, 2, 3
+    P_ = PTS + gh * gw
+    npatch = gh * gw
+    k = (torch.randn(B, H, S * P_, 64, generator=g, device=dev) * 0.7).bfloat16()
+    v = torch.randn(B, H, S * P_, 64, generator=g, device=dev).bfloat16()
+    seeds_pos = [(y * gw + x) for y in range(0, gh, kp) for x in range(0, gw, kp)]
+    kv = k.view(B, H, S, P_, 64)
+    for j in (1, 2, 3):
+        kv[:, :, :, PTS + seeds_pos[j]] = kv[:, :, :, PTS + seeds_pos[0]]
+    pk, pv, size, assign = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, True)
+    npool = len(seeds_pos)
+    a = assign.cpu().long().reshape(-1, npatch)
+    cnt = torch.nn.functional.one_hot(a, npool).double().sum(1)
+    assert torch.equal(size.cpu().reshape(-1, npool).double(), cnt)
+    assert (cnt[:, 1:4] == 0).all() and (cnt[:, 0] >= 4).all()
+    kp5 = k.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+    vp5 = v.view(B, H, S, P_, 64)[:, :, :, PTS:].reshape(-1, npatch, 64).cpu()
+    onehot = torch.nn.functional.one_hot(a, npool).double()
+    for got, rows in ((pk, kp5), (pv, vp5)):
+        want = torch.einsum("gps,gpd->gsd", onehot, rows.double()) / cnt.clamp_min(1)[..., None]
+        got = got.cpu().double().reshape(-1, npool, 64)
+        assert (got[:, 1:4] == 0).all()
+        err = (got - want).abs()
+        assert (err <= 2.0 ** -8 * want.abs() + 1e-6).all(), f"max err {err.max().item():.3e}"
+    pk2, pv2, size2, _ = torch.ops.gpa.pool_shared(k, v, S, PTS, gh, gw, kp, False)
+    assert torch.equal(pk2, pk) and torch.equal(pv2, pv) and torch.equal(size2, size)
+
+
 @pytest.mark.parametrize("gh,gw,kp", [(37, 37, 8), (28, 37, 5), (37, 37, 3)])
 def test_pool_shared_kernel_fp16(dev, gh, gw, kp):
     """The fp16 instantiation (the pooling under fp16 autocast): assignment
