@@ -417,6 +417,22 @@ __global__ __launch_bounds__(kAThreads, HD >= 256 ? 1 : 2) void attn_tiled_kerne
     __syncthreads();                          // ... for every wave
     issue(t + 3, dst);
     const f32x16 s_nxt = scores(nxt);
+    // The V^T fragments of tile t, all read before the softmax (read after
+    // it, their LDS latency sat between the softmax and the P.V product:
+    // head dim 256 45.2 -> 35.6 ms, 128 32.5 -> 31.5 ms, same box).
+    bf16x8 vf[DB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        typedef short i16x4 __attribute__((ext_vector_type(4)));
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)&cur.v[v_off[db] + 16 * s * HD]);
+        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)&cur.v[v_off[db] + (16 * s + 8) * HD]);
+        const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
+        vf[db][s] = bf16x8{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
+      }
     // Softmax of S(t): move the offset only where the row max left the window.
     const float mx = row_max(s_cur);
     const bool move = mx > m + kLazyUp<F16>;
@@ -444,16 +460,7 @@ __global__ __launch_bounds__(kAThreads, HD >= 256 ? 1 : 2) void attn_tiled_kerne
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        typedef short i16x4 __attribute__((ext_vector_type(4)));
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&cur.v[v_off[db] + 16 * s * HD]);
-        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)&cur.v[v_off[db] + (16 * s + 8) * HD]);
-        const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), u4 = __builtin_bit_cast(bf16x4, up);
-        const bf16x8 vf{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]};
-        o_acc[db] = mfma32x32x16_t<F16>(vf, pb[s], o_acc[db]);
-      }
+      for (int s = 0; s < 2; ++s) o_acc[db] = mfma32x32x16_t<F16>(vf[db][s], pb[s], o_acc[db]);
     s_cur = s_nxt;
   };
   for (int t = 0; t < ntiles; t += 4) {
