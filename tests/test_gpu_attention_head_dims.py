@@ -126,3 +126,23 @@ def test_late_key_moves_the_offset(dev, D, dtype, rise):
     k[:, :, N - 7] = alpha * u                        # score ~ rise log2 units
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     _check(dev, q, k, v, b, D, tight=False)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_rows_past_n_never_reach_the_output(dev, D):
+    """k and v are views of longer buffers whose rows past N hold NaN: the
+    tiled kernel's range-checked DMA must read zeros there (the last tile is
+    partial, N = 1000 = 31 x 32 + 8), so the output equals that of
+    contiguous copies bit for bit and matches the oracle."""
+    B, H, M, N = 1, 2, 300, 1000
+    q, k, v, b = _inputs(B, H, M, N, D, seed=D + 1, dtype=torch.bfloat16)
+    kf = torch.full((B, H, N + 96, D), float("nan"), dtype=torch.bfloat16)
+    vf = torch.full((B, H, N + 96, D), float("nan"), dtype=torch.bfloat16)
+    kf[:, :, :N] = k
+    vf[:, :, :N] = v
+    kd, vd = kf.to(dev), vf.to(dev)
+    o_view, lse_view = attention_keybias(q.to(dev), kd[:, :, :N], vd[:, :, :N], b.to(dev),
+                                         D ** -0.5, return_lse=True)
+    o_copy = _check(dev, q, k, v, b, D)
+    assert torch.isfinite(o_view.float()).all() and torch.isfinite(lse_view).all()
+    assert torch.equal(o_view.view(torch.int16), o_copy.view(torch.int16))
