@@ -390,3 +390,21 @@ def test_hot_kernels_have_no_spills_or_scratch():
     assert len(attn) == 2 and all(u["occupancy"] >= 2 for u in attn), attn
     tiled = [u for n, u in report["attn_any_dim.hip"].items() if "attn_tiled_kernelILi128" in n]
     assert len(tiled) == 2 and all(u["occupancy"] >= 2 for u in tiled), tiled
+
+
+def test_bench_measures_one_gpu_and_prices_against_the_bf16_peak(capsys):
+    """bench.py refuses N > 1 with a message (one GPU carries the whole
+    path here), and a kernel entry's TFLOP/s and % of peak follow from the
+    FLOP count and the time against the 2,516.6 TFLOP/s dense bf16 peak."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "bench_mod", Path(__file__).resolve().parent.parent / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "one GPU" in capsys.readouterr().err
+    e = bench.kernel_entry(7.7327400960e13, 64.0)
+    assert abs(e["tflops"] - 7.7327400960e13 / 64e-3 / 1e12) < 0.01
+    assert abs(e["pct_peak"] - 100 * e["tflops"] / 2516.6) < 0.01
+    args = bench.parse_args([])
+    assert args.gpus == 1 and args.steps > 0 and args.warmup >= 0
