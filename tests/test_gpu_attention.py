@@ -392,3 +392,64 @@ def test_tile0_offset_layernorm_scale(dev, dtype):
     else:
         assert (f == 0).all()
         assert (l.cpu() - ref_lse).abs().max().item() < LSE_TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bias", ["none", "log_counts"])
+def test_frame_shape_many_batch_heads(dev, dtype, bias):
+    """640 batch-heads of 1,374 queries (five full 256-query blocks and a
+    last one of 94 rows), the frame-attention shape, with a ragged key count:
+    a sample of batch-heads, the last included, matches the reference in
+    output and LSE.  In every batch-head's last block waves 2 and 3 hold no
+    queries (flag 0 or ATTN_FLAG_RERUN), and without a bias (no score bound)
+    waves 0 and 1 -- 64 and 30 live rows -- show which offset they took."""
+    B, H, M, N = 40, 16, 1374, 777
+    g = torch.Generator().manual_seed(77)
+    q = (torch.randn(B, H, M, 64, generator=g) * 0.5).to(dtype)
+    k = (torch.randn(B, H, N, 64, generator=g) * 0.5).to(dtype)
+    v = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    b = None
+    if bias == "log_counts":
+        counts = torch.randint(1, 9, (B, 1, 1, N), generator=g).float()
+        b = counts.log().expand(B, H, 1, N).to(dtype).contiguous()
+    o, l, flags = _native.attn_keybias_offset_flags(q.to(dev), k.to(dev), v.to(dev),
+                                                    None if b is None else b.to(dev), 0.125, True)
+    assert flags.shape == (B * H, 6, 4)
+    f = flags.cpu()
+    assert (f[:, 5, 2:] == (f[:, 5, 2:] & _native.ATTN_FLAG_RERUN)).all()
+    if bias == "none" and dtype == torch.bfloat16:
+        assert ((f[:, :, :2] & (_native.ATTN_FLAG_TILE0 | _native.ATTN_FLAG_LAZY)) != 0).all()
+    lse_tol = LSE_TOL if dtype == torch.bfloat16 else 2.0 ** -10 / math.log(2.0) + 1e-5
+    for bh in (0, 1, 17, 333, B * H - 1):
+        bi, hi = divmod(bh, H)
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref, ref_lse = attention_reference(q[sl].float(), k[sl].float(), v[sl].float(),
+                                           None if b is None else b[sl].float(), 0.125)
+        err = (o[sl].float().cpu() - ref).abs()
+        assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS, (bh, err.max())
+        assert (l[sl].cpu() - ref_lse).abs().max().item() < lse_tol, bh
+    assert torch.isfinite(o.float()).all()
+
+
+@pytest.mark.parametrize("dtype,X", [(torch.bfloat16, 300.0), (torch.float16, 26.0)])
+def test_short_query_block_tile0_overflow_recomputes(dev, dtype, X):
+    """120 queries (one workgroup: waves 0 and 1 hold 64 and 56 rows, waves 2
+    and 3 none) whose tile-0 offsets all pass the narrow-span test; row 10
+    meets a key aligned with its query in tile 7, its P overflows, and the
+    workgroup streams the keys again with the lazily moved offset, the waves
+    without queries carrying their share of the DMAs.  Outputs and LSE match
+    the reference."""
+    M, N = 120, 1000
+    q, k, v = _aligned_inputs(M, N, X, [(10, 7 * 32 + 5)], seed=33, dtype=dtype)
+    args = [t.to(dev, dtype) for t in (q, k, v)]
+    o, l, flags = _native.attn_keybias_offset_flags(*args, None, 0.125, True)
+    ref, ref_lse = attention_reference(q, k, v, None, 0.125)
+    err = (o.float().cpu() - ref).abs()
+    assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    lse_tol = LSE_TOL if dtype == torch.bfloat16 else 2.0 ** -10 / math.log(2.0) + 1e-5
+    assert (l.cpu() - ref_lse).abs().max().item() < lse_tol
+    f = flags.cpu()
+    T0, LZ, RR = _native.ATTN_FLAG_TILE0, _native.ATTN_FLAG_LAZY, _native.ATTN_FLAG_RERUN
+    assert f.shape == (2, 1, 4)
+    assert (f[:, 0, :2] == T0 | LZ | RR).all()          # tile-0 offset, then recomputed
+    assert (f[:, 0, 2:] == RR).all()                    # no queries, streamed twice
