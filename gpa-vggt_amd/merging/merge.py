@@ -4,7 +4,8 @@ Drop-in for the reference's `merging/merge.py`: `token_merge_bipartite2d`
 keeps its signature and returns the same closure (`merge(x, mode)`,
 `merge.heads(t, mode)`, `merge.size`), and `PROJ_SEED` keeps its value.
 The similarity step always runs the gfx950 kernel (`fused_similarity_argmax`);
-there is no chunked-bmm fallback.
+there is no chunked-bmm fallback.  `fast_similarity_chunks` keeps the
+reference's name and arguments (reference :13-36) and runs the same kernel.
 
 Orderings the reference leaves to torch's sort are fixed here:
   * dst / src order (reference :165): tokens in increasing position within
@@ -45,7 +46,8 @@ import torch
 from . import _native
 from .fused_similarity import fused_similarity_argmax
 
-__all__ = ["token_merge_bipartite2d", "PROJ_SEED", "dst_mask", "num_dst_tokens"]
+__all__ = ["token_merge_bipartite2d", "fast_similarity_chunks", "PROJ_SEED", "dst_mask",
+           "num_dst_tokens"]
 
 # Seed of the fixed Gaussian basis used by the metric_dim random projection
 # (reference merging/merge.py:10).
@@ -98,6 +100,35 @@ def dst_mask(num_imgs: int, w: int, h: int, sx: int, sy: int, num_special: int,
     pos = starts.view(-1, 1, 1) + num_special + ys * row_len + xs
     mask[pos.reshape(-1)] = -1
     return mask
+
+
+def fast_similarity_chunks(a: torch.Tensor, b_transposed: torch.Tensor,
+                           chunk_size: int):
+    """node_max, node_idx of a @ b_transposed, under the reference's name
+    and arguments (merging/merge.py:13-36), on the fused gfx950 kernel.
+
+    a [B, M, C], b_transposed [B, C, N] on the GPU (fp32, bf16 or fp16).
+    Like the reference, both operands are cast to bf16 whatever their dtype
+    (:22-23) and node_max comes back as a bf16 value in a's dtype (:31-33);
+    node_idx is int64.  No chunk of scores is materialised, so `chunk_size`
+    (which must be positive, as the reference's `range` step) does not change
+    the result.  The reference takes the max over bf16-rounded scores, this
+    kernel over the fp32 scores and rounds the max once: rounding is
+    monotonic, so the two maxima agree up to the order in which each sums a
+    score's products, and node_idx differs from the reference's only where
+    two destinations round to the same bf16 score
+    (merging/fused_similarity.py:86 states the same of its own kernel).
+    """
+    if chunk_size <= 0:
+        raise ValueError(f"fast_similarity_chunks: chunk_size must be positive, got {chunk_size}")
+    if not (a.dim() == 3 and b_transposed.dim() == 3):
+        raise AssertionError(
+            "fast_similarity_chunks expects a [B, M, C] and b_transposed [B, C, N] "
+            f"(got {tuple(a.shape)} and {tuple(b_transposed.shape)})")
+    out_dtype = a.dtype
+    node_max, node_idx = fused_similarity_argmax(
+        a.to(torch.bfloat16), b_transposed.transpose(-1, -2).to(torch.bfloat16).contiguous())
+    return node_max.to(out_dtype), node_idx
 
 
 _PROJ_CACHE: dict = {}

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|sharp|own|shared|merge|front|pool|qk|combine|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|core|sharp|own|shared|merge|front|pool|qk|combine|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
@@ -22,6 +22,8 @@
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
   pool4  the same at pool stride 4: 100 seeds per frame, the super-chunked
          kernel (not in `all`)
+  core   biased attention at the 200-frame core-block shape: 16 heads x
+         274,800 queries x 219,840 merged keys (not in `all`)
   attn128 attention at head dim 128: 16 heads x 65,536 queries x 68,700 keys,
          log-count bias (the tiled kernel; not in `all`)
   qk     qk LayerNorm + 2D RoPE of a 200-frame block: the bf16 QKV projection
@@ -57,7 +59,7 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "sim200", "sim1024", "attn", "sharp", "own", "shared", "merge", "front",
+    if which not in ("sim", "sim200", "sim1024", "attn", "core", "sharp", "own", "shared", "merge", "front",
                      "pool", "pool4", "attn128", "qk", "combine", "sim16", "attn16", "attn0",
                      "copy", "all"):
         print(__doc__, file=sys.stderr)
@@ -142,6 +144,13 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"pool4 16x200 frames kp 4 (100 seeds) x {reps} done", flush=True)
         del kk, vv
+    if which == "core":
+        q, k, v, b = W.attn_inputs(m=274_800, n=219_840, device=dev)
+        for _ in range(reps):
+            attention_keybias(q, k, v, b, 0.125)
+        torch.cuda.synchronize()
+        print(f"core 16x274800x219840x64 x {reps} done", flush=True)
+        del q, k, v, b
     if which == "attn128":
         q, k, v, b = W.attn_inputs(m=274_800, n=68_700, d=128, device=dev)
         q = q[:, :, :65_536].contiguous()

@@ -253,3 +253,28 @@ def test_max_written_in_the_input_dtype(dev, dtype):
     fmax, fidx = torch.ops.gpa.sim_argmax(a.to(dev), b.to(dev))
     assert vmax.dtype == dtype and fmax.dtype == torch.float32
     assert torch.equal(vmax, fmax.to(dtype)) and torch.equal(vidx, fidx)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_merge_module_fast_similarity_chunks(dev, dtype):
+    """merging.merge.fast_similarity_chunks keeps the reference's name and
+    arguments (merging/merge.py:13-36: a [B, M, C], b transposed [B, C, N],
+    a chunk size) on the fused kernel: both operands cast to bf16 whatever
+    their dtype, node_max a bf16 value returned in a's dtype, node_idx int64;
+    against the oracle's restatement of the reference path under the gap
+    rule, the max within one bf16 ulp, and no dependence on the chunk size."""
+    from merging.merge import fast_similarity_chunks as product_chunks
+    a = _unit_bf16_values((2, 3000, 128), seed=81).to(dtype)
+    b = _unit_bf16_values((2, 5000, 128), seed=82).to(dtype)
+    bt = b.transpose(1, 2)
+    vmax, vidx = product_chunks(a.to(dev), bt.to(dev), 5000)
+    assert vmax.dtype == dtype and vidx.dtype == torch.int64
+    assert torch.equal(vmax.float(), vmax.float().bfloat16().float())    # a bf16 value
+    rmax, ridx = fast_similarity_chunks(a, bt, 1000)
+    gap = bf16_top2_gap(a.bfloat16().float(), b.bfloat16().float())
+    keep = gap >= 1e-3
+    assert keep.float().mean() > 0.5
+    assert torch.equal(vidx.cpu()[keep], ridx[keep])
+    assert (vmax.float().cpu() - rmax.float()).abs().max().item() <= 2 ** -7
+    vmax2, vidx2 = product_chunks(a.to(dev), bt.to(dev), 7)
+    assert torch.equal(vmax2, vmax) and torch.equal(vidx2, vidx)

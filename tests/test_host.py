@@ -16,6 +16,7 @@ import torch
 
 from merging import _native
 from merging.merge import dst_mask, num_dst_tokens, token_merge_bipartite2d
+from merging.merge import fast_similarity_chunks as merge_fast_similarity_chunks
 from merging.fused_similarity import fused_similarity_argmax
 from merging.fused_attention import attention_keybias, LOG2E
 from oracle.merge import build_dst_mask, window_draw
@@ -352,6 +353,19 @@ def test_cpu_tensors_are_refused():
         token_merge_bipartite2d(torch.randn(1, 2 * 41, 32), 6, 6, 2, 2, 5)
     with pytest.raises(ValueError):
         token_merge_bipartite2d(torch.randn(1, 2 * 41, 32), 6, 6, 2, 2, 0)
+    with pytest.raises(AssertionError):
+        merge_fast_similarity_chunks(a, a.transpose(1, 2), 5000)
+
+
+def test_merge_fast_similarity_chunks_argument_errors():
+    """The reference's chunked entry point keeps its argument checks: a
+    non-positive chunk size (the reference's `range` step) and operands
+    that are not [B, M, C] / [B, C, N]."""
+    a = torch.randn(1, 8, 128)
+    with pytest.raises(ValueError):
+        merge_fast_similarity_chunks(a, a.transpose(1, 2), 0)
+    with pytest.raises(AssertionError):
+        merge_fast_similarity_chunks(a[0], a.transpose(1, 2), 5000)
 
 
 def test_log2e_constant():
