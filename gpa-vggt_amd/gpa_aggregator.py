@@ -315,6 +315,7 @@ class GpaAttention(nn.Module):
         own_v = v5[:, :, :, pts:].permute(0, 2, 1, 3, 4).reshape(B * S, H, P - pts, D)
         out_a, lse_a = attention_keybias(q_f, own_k, own_v, None, self.scale, return_lse=True)
         del own_k, own_v
+        self._mark("frame_special_attn")
         if kp > 0:
             pooled_k, pooled_v, pool_size, _ = pool_shared_set(k, v, S, pts, gh, gw, kp)
             if self.merge_log is not None:
