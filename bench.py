@@ -69,7 +69,8 @@ def e2e_latency(dev) -> dict:
       global blocks on the GPA schedule) on 200 frames of 518 x 518 images,
       with the reference defaults, and with the variant of 64 pooled patch
       summaries per frame in the shared set (pool stride 5) and every merged
-      block at 25 % keep (no core blocks);
+      block at 25 % keep (no core blocks), and with the unprojected 1024-d
+      merge metric (`--merge_metric_dim 0`, eval/eval_co3d.py:121-122);
     * the same aggregator without GPA (vanilla VGGT) and, with the reference
       defaults, as the fp16 accuracy-evaluation stack.
     Timing follows eval/bench_e2e.py: 2 warm-up calls, mean of 3 (1 and 2 for
@@ -105,7 +106,8 @@ def e2e_latency(dev) -> dict:
     frames = 200
     imgs = A.shifted_texture_images(frames, device=dev).to(bf16)
     variants = (("reference_defaults", cfg, model),
-                ("pool64_keep25", A.GpaConfig(broadcast_pool=5, core_blocks=()), None))
+                ("pool64_keep25", A.GpaConfig(broadcast_pool=5, core_blocks=()), None),
+                ("metric_dim0", A.GpaConfig(merge_metric_dim=0), None))
     for tag, c, m in variants:
         if m is None:
             m = A.build_aggregator(c, device=dev)
@@ -123,7 +125,8 @@ def e2e_latency(dev) -> dict:
             "tflop": {k: round(v / 1e12, 2) for k, v in flops.items()},
             "schedule": {"early_frame_split": c.early_frame_split, "broadcast_pool": c.broadcast_pool,
                          "merge": [c.merging, c.merge_end, c.merge_ratio],
-                         "core_blocks": list(c.core_blocks), "core_merge_ratio": c.core_merge_ratio}}
+                         "core_blocks": list(c.core_blocks), "core_merge_ratio": c.core_merge_ratio,
+                         "merge_metric_dim": c.merge_metric_dim}}
         log(f"[bench] aggregator 200 frames ({tag}): {ms:.1f} ms")
         del m
         torch.cuda.empty_cache()

@@ -685,8 +685,12 @@ def aggregator_flops(cfg: GpaConfig, frames: int) -> Dict[str, float]:
             ns = T - nd
             r = min(ns, int(T * cfg.block_merge_ratio(i)))
             out["global_attn"] += 4.0 * cfg.num_heads * T * (T - r) * Hd
-            out["similarity"] += 2.0 * ns * nd * cfg.merge_metric_dim
-            out["dense"] += 2.0 * T * C * cfg.merge_metric_dim
+            # The metric is projected to merge_metric_dim features only when
+            # that is a reduction (merge.py:180); else the C-d cosine runs.
+            projected = 0 < cfg.merge_metric_dim < C
+            out["similarity"] += 2.0 * ns * nd * (cfg.merge_metric_dim if projected else C)
+            if projected:
+                out["dense"] += 2.0 * T * C * cfg.merge_metric_dim
         else:
             out["global_attn"] += 4.0 * cfg.num_heads * T * T * Hd
     return out

@@ -183,6 +183,16 @@ def test_aggregator_flops_closed_form():
     assert f["frame_attn"] == pytest.approx(48 * 4.0 * 200 * H * 1374 * 1374 * D, rel=1e-12)
 
 
+def test_aggregator_flops_unprojected_metric():
+    """merge_metric_dim=0 (eval/eval_co3d.py:121-122): no projection GEMM,
+    the similarity over all 1024 features."""
+    base = A.aggregator_flops(A.GpaConfig(), 200)
+    f = A.aggregator_flops(A.GpaConfig(merge_metric_dim=0), 200)
+    assert f["similarity"] == pytest.approx(15 * 2.0 * 207_955 * 66_845 * 1024, rel=1e-12)
+    assert base["dense"] - f["dense"] == pytest.approx(15 * 2.0 * 274_800 * 1024 * 128, rel=1e-12)
+    assert f["global_attn"] == base["global_attn"]
+
+
 def test_aggregator_flops_rectangular_and_frame_only():
     """392 x 518 images (28 x 37 patches): 20 pooled summaries per frame at
     kp 8; kp < 0 is plain attention over each frame's own tokens."""

@@ -231,6 +231,36 @@ def test_small_aggregator_runs_every_global_path(dev, hw, dt):
     assert flops["similarity"] > 0 and flops["global_attn"] > 0
 
 
+def test_small_aggregator_unprojected_metric(dev):
+    """merge_metric_dim=0 (eval/eval_co3d.py:121-122): the merged blocks
+    match tokens on the full 1024-d cosine (the 256 x 256-tile similarity
+    kernel above 256 destinations, no projection or fused front end);
+    finite outputs, bit-identical on a second forward, every merge keeping
+    all tokens (sizes sum to the token count) and merging r of them."""
+    cfg = A.GpaConfig(depth=3, vit_depth=1, early_frame_split=1, merging=1,
+                      core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2),
+                      merge_metric_dim=0)
+    P = cfg.tokens_per_frame
+    model = A.build_aggregator(cfg, device=dev, seed=3)
+    imgs = A.shifted_texture_images(FRAMES, device=dev).to(torch.bfloat16)
+    log = []
+    model.set_merge_log(log)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outs = model(imgs)
+    model.set_merge_log(None)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        again = model(imgs)
+    assert all(torch.equal(a, b) for a, b in zip(outs, again))
+    for o in outs:
+        assert o.shape == (1, FRAMES, P, 2048) and torch.isfinite(o).all()
+    merged = [r for r in log if r["kind"] == "merged"]
+    assert len(merged) == 2
+    for rec in merged:
+        T = rec["tokens"]
+        assert int(rec["size"].sum().item()) == T
+        assert rec["keys"] == T - int(rec["r"])
+
+
 @pytest.mark.parametrize("frames,k_f32,half", [(3, True, torch.bfloat16), (2, False, torch.bfloat16),
                                                (3, True, torch.float16), (2, False, torch.float16)])
 def test_qk_norm_rope_kernel_matches_textbook(dev, frames, k_f32, half):
