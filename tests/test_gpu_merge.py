@@ -129,3 +129,37 @@ def test_config1_end_to_end(dev):
     print(f"\n[config1] N_m={km.shape[2]} max-abs {err.max().item():.3e} "
           f"mean-abs {err.mean().item():.3e}")
     assert err.max().item() <= 2e-2 and err.mean().item() <= 5e-3
+
+
+@pytest.mark.parametrize("mdim", [128, 0])
+def test_batched_merge_equals_per_element_merges(dev, mdim):
+    """A batch of two scenes (the reference takes B > 1, merging/merge.py:
+    39-256; `merge.size` is then None and the caller sums ones,
+    vggt/layers/attention.py:250-253): every batch element's merge equals
+    the merge of that element alone, bit for bit (node indices, assignment,
+    merged K/V), and the summed sizes equal the single-scene sizes."""
+    frames, w, h, ns, c = 3, 37, 37, 5, 1024
+    n = frames * (w * h + ns)
+    metric = torch.cat([W.shifted_basis_tokens(frames, dim=c, seed=s)[:, :n] for s in (3, 4)])
+    r = int(0.98 * n)
+
+    def merged(x):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(33)
+        return token_merge_bipartite2d(x.to(dev), w, h, 2, 2, r, False, gen, metric_dim=mdim,
+                                       num_special=ns)
+
+    mb = merged(metric)
+    assert mb.size is None
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(2, 4, n, 64, generator=g).to(dev)
+    v = torch.randn(2, 4, n, 64, generator=g).bfloat16().to(dev)
+    kb, vb = mb.heads(k, "mean"), mb.heads(v, "mean")
+    sizes = mb(torch.ones(2, n, 1, device=dev), "sum")[..., 0]
+    for e in range(2):
+        m1 = merged(metric[e:e + 1])
+        for name in ("node_idx", "dst_idx", "unm_abs_idx", "src_abs_idx"):
+            assert torch.equal(getattr(mb.index, name)[e], getattr(m1.index, name)[0]), name
+        assert torch.equal(sizes[e], m1.size[0])
+        assert torch.equal(kb[e], m1.heads(k[e:e + 1], "mean")[0])
+        assert torch.equal(vb[e], m1.heads(v[e:e + 1], "mean")[0])
