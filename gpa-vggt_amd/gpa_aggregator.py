@@ -277,7 +277,12 @@ class GpaAttention(nn.Module):
                                        "num_dst": m.index.num_dst, "r": m.index.r,
                                        "size": m.size, "slot_offsets": m.index.slot_offsets,
                                        "keys": k.shape[2]})
-            bias = m.size.reshape(B, 1, 1, -1).log().to(q.dtype).expand(B, H, 1, k.shape[2])
+            size = m.size
+            if size is None:
+                # More than one scene: the sizes as the reference forms them
+                # (vggt/layers/attention.py:250-253), summed ones.
+                size = m(torch.ones(B, N, 1, device=x.device, dtype=torch.float32), "sum")
+            bias = size.reshape(B, 1, 1, -1).log().to(q.dtype).expand(B, H, 1, k.shape[2])
             self._mark("merge")
             out = attention_keybias(q, k, v, bias, self.scale)
             self._mark("merged_attn")

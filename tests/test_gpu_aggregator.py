@@ -231,6 +231,28 @@ def test_small_aggregator_runs_every_global_path(dev, hw, dt):
     assert flops["similarity"] > 0 and flops["global_attn"] > 0
 
 
+def test_small_aggregator_two_scenes(dev):
+    """A batch of two scenes ([2, S, 3, H, W] images, as the reference's
+    aggregator takes them): the merged blocks take their key sizes from
+    summed ones (vggt/layers/attention.py:250-253) since `merge.size` is
+    None; the same scene twice gives bit-identical outputs for both batch
+    elements, close to the one-scene forward (the dense GEMMs may run other
+    kernels for twice the rows)."""
+    cfg = A.GpaConfig(depth=3, vit_depth=1, early_frame_split=1, merging=1,
+                      core_blocks=(2,), core_merge_ratio=0.5, dpt_blocks=(0, 1, 2))
+    P = cfg.tokens_per_frame
+    model = A.build_aggregator(cfg, device=dev, seed=2)
+    img = A.shifted_texture_images(FRAMES, device=dev).to(torch.bfloat16)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        two = model(torch.cat([img, img]))
+        one = model(img)
+    for o2, o1 in zip(two, one):
+        assert o2.shape == (2, FRAMES, P, 2048) and torch.isfinite(o2).all()
+        assert torch.equal(o2[0], o2[1])
+        d = (o2[0].float() - o1[0].float()).abs()
+        assert d.mean().item() <= 1e-2 * o1.float().abs().mean().item()
+
+
 def test_small_aggregator_unprojected_metric(dev):
     """merge_metric_dim=0 (eval/eval_co3d.py:121-122): the merged blocks
     match tokens on the full 1024-d cosine (the 256 x 256-tile similarity
