@@ -453,3 +453,28 @@ def test_short_query_block_tile0_overflow_recomputes(dev, dtype, X):
     assert f.shape == (2, 1, 4)
     assert (f[:, 0, :2] == T0 | LZ | RR).all()          # tile-0 offset, then recomputed
     assert (f[:, 0, 2:] == RR).all()                    # no queries, streamed twice
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_keys_masked_by_minus_inf_bias(dev, dtype, D):
+    """A -inf bias masks a key (the reference's `qk + bias` gives -inf and
+    exp2 gives 0, fused_attention.py:106-111): here the first two key tiles
+    of every row (64 keys) and a random third of the rest are masked, so the
+    first tiles every wave scores carry no live key and the offset has to
+    come from later tiles.  Against the fp32 reference on the same inputs."""
+    B, H, M, N = 1, 2, 300, 1000
+    g = torch.Generator().manual_seed(D)
+    q = (torch.randn(B, H, M, D, generator=g) * 0.5).to(dtype)
+    k = (torch.randn(B, H, N, D, generator=g) * 0.5).to(dtype)
+    v = torch.randn(B, H, N, D, generator=g).to(dtype)
+    b = torch.randint(1, 9, (B, H, 1, N), generator=g).float().log()
+    masked = torch.rand(B, H, 1, N, generator=g) < 1 / 3
+    masked[..., :64] = True
+    b = b.masked_fill(masked, float("-inf"))
+    o, lse = attention_keybias(q.to(dev), k.to(dev), v.to(dev), b.to(dev), D ** -0.5,
+                               return_lse=True)
+    ref, ref_lse = attention_reference(q, k, v, b, D ** -0.5)
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    _check(o, ref)
+    assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
