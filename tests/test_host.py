@@ -39,6 +39,40 @@ def test_library_exports_every_declared_function():
     assert set(declared) == set(_native.exported_symbols())
 
 
+def test_header_is_c99_and_links(tmp_path):
+    """A C caller: the header compiles as C99 with warnings as errors, every
+    declared function links against the built library by the header's
+    prototype, and a call that fails argument validation returns the
+    documented code and message without touching a GPU."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    names = _declared_functions()
+    src = tmp_path / "abi.c"
+    src.write_text(
+        "#include <stdio.h>\n#include \"gpa_mi355x.h\"\n"
+        "int main(void) {\n"
+        "  typedef void (*fn_t)(void);\n"
+        "  const fn_t fns[] = {" + ", ".join(f"(fn_t)&{n}" for n in names) + "};\n"
+        "  int rc = gpa_sim_argmax_bf16(0, 0, 0, GPA_DTYPE_F32, 0, 1, -1, 1, 128, 0, 0, 0, 0,"
+        " 0, 0, 0, 0, 0);\n"
+        "  printf(\"%d %d %d %s\\n\", gpa_abi_version(), GPA_ABI_VERSION, rc,"
+        " gpa_last_error());\n"
+        "  return fns[0] == 0;\n}\n")
+    lib_dir = _native.LIB_PATH.parent
+    exe = tmp_path / "abi"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{HEADER.parent}",
+                    str(src), "-o", str(exe), f"-L{lib_dir}", "-lgpa_mi355x",
+                    f"-Wl,-rpath,{lib_dir}", "-Wl,-rpath,/opt/rocm/lib"],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert int(out[0]) == int(out[1]) == _native.ABI_VERSION
+    assert int(out[2]) == _native.GPA_E_INVALID
+    assert "negative" in " ".join(out[3:])
+
+
 def test_abi_version_and_empty_error():
     lib = _native.lib()
     assert lib.gpa_abi_version() == _native.ABI_VERSION
