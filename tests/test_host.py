@@ -71,6 +71,15 @@ def test_header_is_c99_and_links(tmp_path):
     assert int(out[0]) == int(out[1]) == _native.ABI_VERSION
     assert int(out[2]) == _native.GPA_E_INVALID
     assert "negative" in " ".join(out[3:])
+    # The C caller INTEGRATION.md shows compiles and links as written.
+    doc = (HEADER.parent.parent / "INTEGRATION.md").read_text()
+    snippet = re.search(r"```c\n(.*?)```", doc, re.S).group(1)
+    (tmp_path / "doc.c").write_text(snippet + "\nint main(void) { return 0; }\n")
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                    "-I/opt/rocm/include", f"-I{HEADER.parent}", str(tmp_path / "doc.c"),
+                    "-o", str(tmp_path / "doc"), f"-L{lib_dir}", "-lgpa_mi355x",
+                    "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"],
+                   check=True, capture_output=True, text=True)
 
 
 def test_abi_version_and_empty_error():
