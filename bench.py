@@ -12,7 +12,8 @@ similarity, the frame-special calls, the HBM-bound kernels around the path,
 the fp16 twins, and attention on larger logits -- LayerNorm-scale and sharp
 q/k -- with the shares of waves on the tile-0 and the lazily moved softmax
 offsets), the practical MFMA ceiling (a hipBLASLt bf16 GEMM on random and on
-all-zero data), the end-to-end latency of one GPA block (100
+all-zero data, and register-only probes of the MFMA shapes and of the
+attention's own instruction mix), the end-to-end latency of one GPA block (100
 frames) and of the whole aggregator (200 frames) on the random-init VGGT-1B
 harness for the GPA schedule and for vanilla VGGT, the roofline of the
 dominant kernel and a CPU baseline (the torch restatement of the reference
@@ -39,6 +40,7 @@ PEAK_BF16_TFLOPS = 2516.6     # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 
 HBM_BYTES_PER_S = 8.0e12      # MI355X HBM3E
 SM_SCALE = 64 ** -0.5
 TRAFFIC_FILE = REPO / "profiles" / "attn_keybias_traffic.json"
+PROBE_LIB = REPO / "gpa-vggt_amd" / "merging" / "_lib" / "libgpa_probe.so"
 
 
 def log(msg: str) -> None:
@@ -242,6 +244,48 @@ def attention_floor(q, k, v, bias, biased_ms: float) -> dict:
     if "ms" in nb:
         out["bias_overhead_pct"] = round(100.0 * (biased_ms / nb["ms"] - 1.0), 2)
     return out
+
+
+def mix_ceiling(dev) -> dict:
+    """What the power limit leaves for an instruction mix, from the
+    register-only probes of csrc/probe/mfma_mix_probe.hip (no memory traffic
+    in the loop; two waves per SIMD as the attention runs): 32x32x16 and
+    16x16x32 bf16 MFMAs alone, and one key tile of the attention main loop
+    (its 16 MFMAs of 32x32x16, row-sum MFMAs and softmax VALU work, FLOPs
+    counted as the attention counts them), each on random operands and on
+    all-zero ones.  {} when the probe library is not built."""
+    import ctypes
+
+    import torch
+    if not PROBE_LIB.exists():
+        log(f"[bench] {PROBE_LIB.name} not built: no instruction-mix ceiling")
+        return {}
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.gpa_probe_mfma_mix.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.gpa_probe_flops.restype = ctypes.c_double
+    lib.gpa_probe_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+    nsrc = 1 << 20                                   # 16-byte fragments
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    srcs = {"random": (torch.rand(nsrc * 8, generator=g, device=dev) * 2 - 1).bfloat16(),
+            "zeros": torch.zeros(nsrc * 8, device=dev, dtype=torch.bfloat16)}
+    out = torch.empty(lib.gpa_probe_threads(), device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    for mode, iters, name in ((0, 600_000, "mfma_32x32x16"), (1, 600_000, "mfma_16x16x32"),
+                              (2, 250_000, "attention_tile_mix")):
+        for tag, src in srcs.items():
+            def fn(mode=mode, src=src, iters=iters):
+                rc = lib.gpa_probe_mfma_mix(mode, src.data_ptr(), nsrc, out.data_ptr(), iters,
+                                            stream)
+                if rc != 0:
+                    raise RuntimeError(f"gpa_probe_mfma_mix mode {mode} returned {rc}")
+            fn()
+            t = statistics.median(event_ms(fn, 3))
+            res[f"probe_{name}_{tag}"] = kernel_entry(lib.gpa_probe_flops(mode, iters), t)
+    del srcs, out
+    return res
 
 
 def kernel_entry(flops: float, ms: float) -> dict:
@@ -623,6 +667,10 @@ def main(argv=None) -> int:
     torch.cuda.empty_cache()
     gemm_tf = ceiling[f"hipblaslt_gemm_bf16_{n}_randn"]["tflops"]
     log(f"[bench] hipBLASLt GEMM ceiling {gemm_tf:.0f} TFLOP/s on random data")
+    ceiling.update(mix_ceiling(dev))
+    mix_tf = ceiling.get("probe_attention_tile_mix_random", {}).get("tflops")
+    if mix_tf:
+        log(f"[bench] attention instruction mix, registers only: {mix_tf:.0f} TFLOP/s on random data")
 
     achieved = f_attn / (attn_ms * 1e-3) / 1e12
     traffic = None
@@ -636,6 +684,9 @@ def main(argv=None) -> int:
                 "traffic": traffic, "kernel": "attn_main_kernel",
                 "flops_per_launch": f_attn,
                 "gemm_ceiling_tflops": gemm_tf, "frac_of_gemm_ceiling": round(achieved / gemm_tf, 4)}
+    if mix_tf:
+        roofline.update({"mix_ceiling_tflops": mix_tf,
+                         "frac_of_mix_ceiling": round(achieved / mix_tf, 4)})
 
     e2e = None
     if not args.no_e2e:

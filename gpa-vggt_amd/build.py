@@ -129,7 +129,28 @@ def build(report: bool = False, verbose: bool = True) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH.relative_to(REPO_DIR)}")
+    _build_probe(verbose)
     return LIB_PATH
+
+
+PROBE_SRC = CSRC / "probe"
+PROBE_LIB = LIB_DIR / "libgpa_probe.so"
+
+
+def _build_probe(verbose: bool) -> None:
+    """The register-only MFMA probes the benchmark prices its ceilings with
+    (csrc/probe/, a library of its own: not part of the product ABI)."""
+    sources = sorted(PROBE_SRC.glob("*.hip"))
+    if not sources:
+        return
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-shared", "-o", str(tmp), *[str(s) for s in sources]]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on the probes:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB.relative_to(REPO_DIR)}")
 
 
 def main(argv=None) -> int:

@@ -82,6 +82,27 @@ def test_header_is_c99_and_links(tmp_path):
                    check=True, capture_output=True, text=True)
 
 
+def test_probe_library_exports_its_entry_points():
+    """The benchmark's register-only MFMA probes (a library of their own,
+    not part of the product ABI): the three entry points load, argument
+    errors return -1 before any launch, and the FLOP count is the
+    documented one."""
+    probe = _native.LIB_PATH.parent / "libgpa_probe.so"
+    if not probe.exists():
+        pytest.skip("probe library not built")
+    lib = ctypes.CDLL(str(probe))
+    lib.gpa_probe_flops.restype = ctypes.c_double
+    lib.gpa_probe_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.gpa_probe_mfma_mix.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    assert lib.gpa_probe_threads() == 512 * 256
+    assert lib.gpa_probe_flops(0, 10) == 512 * 4 * 10 * 8 * 32768
+    assert lib.gpa_probe_flops(2, 3) == 512 * 4 * 4 * 16 * 32768     # pairs of tiles
+    assert lib.gpa_probe_mfma_mix(3, 1, 1, 1, 1, None) == -1
+    assert lib.gpa_probe_mfma_mix(0, None, 1, 1, 1, None) == -1
+    assert lib.gpa_probe_mfma_mix(0, 1, 1, 1, 0, None) == -1
+
+
 def test_abi_version_and_empty_error():
     lib = _native.lib()
     assert lib.gpa_abi_version() == _native.ABI_VERSION
