@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Run each hot kernel a few times at its benchmark shape, for profilers.
 
-    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|core|sharp|own|shared|merge|front|pool|qk|combine|sim16|attn16|attn0|copy|all} [reps]
+    python3 gpa-vggt_amd/profile_workloads.py {sim|sim200|sim1024|attn|core|probe|sharp|own|shared|merge|front|pool|qk|combine|sim16|attn16|attn0|copy|all} [reps]
 
   sim    fused similarity-argmax, 75,000 x 25,000 x 128 (bf16)
   sim200 the similarity at the 200-frame merge shape, 207,955 x 66,845 x 128
@@ -22,6 +22,9 @@
   pool   pooled shared set: 16 heads x 200 frames x 1369 patches, 25 seeds
   pool4  the same at pool stride 4: 100 seeds per frame, the super-chunked
          kernel (not in `all`)
+  probe  the register-only MFMA probes of csrc/probe/ (32x32x16, 16x16x32,
+         the attention's key tile), each on random and on all-zero
+         operands, in that order (not in `all`)
   core   biased attention at the 200-frame core-block shape: 16 heads x
          274,800 queries x 219,840 merged keys (not in `all`)
   attn128 attention at head dim 128: 16 heads x 65,536 queries x 68,700 keys,
@@ -59,7 +62,7 @@ def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     which = argv[0] if argv else "all"
     reps = int(argv[1]) if len(argv) > 1 else 3
-    if which not in ("sim", "sim200", "sim1024", "attn", "core", "sharp", "own", "shared", "merge", "front",
+    if which not in ("sim", "sim200", "sim1024", "attn", "core", "probe", "sharp", "own", "shared", "merge", "front",
                      "pool", "pool4", "attn128", "qk", "combine", "sim16", "attn16", "attn0",
                      "copy", "all"):
         print(__doc__, file=sys.stderr)
@@ -144,6 +147,12 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"pool4 16x200 frames kp 4 (100 seeds) x {reps} done", flush=True)
         del kk, vv
+    if which == "probe":
+        import bench
+        for _ in range(reps):
+            for name, entry in bench.mix_ceiling(dev).items():
+                print(f"{name}: {entry['ms']:.3f} ms, {entry['tflops']:.0f} TFLOP/s", flush=True)
+        print(f"probe x {reps} done", flush=True)
     if which == "core":
         q, k, v, b = W.attn_inputs(m=274_800, n=219_840, device=dev)
         for _ in range(reps):
