@@ -71,7 +71,7 @@ def test_header_is_c99_and_links(tmp_path):
     assert int(out[0]) == int(out[1]) == _native.ABI_VERSION
     assert int(out[2]) == _native.GPA_E_INVALID
     assert "negative" in " ".join(out[3:])
-    # The C caller INTEGRATION.md shows compiles and links as written.
+    # The C example of the integration guide compiles and links as written.
     doc = (HEADER.parent.parent / "INTEGRATION.md").read_text()
     snippet = re.search(r"```c\n(.*?)```", doc, re.S).group(1)
     (tmp_path / "doc.c").write_text(snippet + "\nint main(void) { return 0; }\n")
