@@ -33,6 +33,8 @@ def _device_draws(dev, frames, w, h, sx, sy, c, mdim, no_rand):
     (4, 37, 37, 2, 2, 5, 1024, 128, 0.2, False),
     (6, 9, 7, 2, 2, 5, 256, 64, 0.5, False),
     (3, 8, 8, 2, 2, 5, 128, 0, 0.98, True),
+    (4, 10, 8, 3, 2, 3, 128, 32, 0.6, False),      # 3 x 2 windows, ragged grid edges
+    (3, 9, 9, 3, 3, 1, 256, 128, 0.98, False),     # 3 x 3 windows, one special token
 ])
 def test_merge_indices_bit_exact_given_node_indices(dev, frames, w, h, sx, sy, ns, c, mdim,
                                                     ratio, no_rand):
