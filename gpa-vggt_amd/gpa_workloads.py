@@ -60,11 +60,13 @@ def projection(dim: int = WIDTH, out_dim: int = 128, seed: int = 1, device="cpu"
 
 
 def sim_inputs(m: int = 75_000, n: int = 25_000, out_dim: int = 128, seed: int = 0,
-               device="cpu") -> Tuple[torch.Tensor, torch.Tensor]:
-    """(src [1, m, out_dim], dst [1, n, out_dim]) bf16, unit rows.
+               device="cpu", dtype=torch.bfloat16) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(src [1, m, out_dim], dst [1, n, out_dim]) in `dtype` (bf16 or fp16),
+    unit rows.
 
     m + n tokens come from `shifted_basis_tokens`, are projected and
-    normalised in fp32; token floor(i * (m + n) / n) is destination i.
+    normalised in fp32, then rounded once to `dtype`; token
+    floor(i * (m + n) / n) is destination i.
     """
     total = m + n
     frames = -(-total // TOKENS_PER_FRAME)
@@ -76,7 +78,7 @@ def sim_inputs(m: int = 75_000, n: int = 25_000, out_dim: int = 128, seed: int =
     is_dst[torch.arange(n, device=device) * total // n] = True
     dst = y[is_dst]
     src = y[~is_dst]
-    return src.to(torch.bfloat16).unsqueeze(0), dst.to(torch.bfloat16).unsqueeze(0)
+    return src.to(dtype).unsqueeze(0), dst.to(dtype).unsqueeze(0)
 
 
 def merge_counts(m: int, n: int, seed: int = 0, device="cpu") -> torch.Tensor:
@@ -89,17 +91,19 @@ def merge_counts(m: int, n: int, seed: int = 0, device="cpu") -> torch.Tensor:
 
 
 def attn_inputs(m: int = 274_800, n: int = 68_700, heads: int = HEADS, d: int = HEAD_DIM,
-                seed: int = 0, device="cpu", bias_dtype=torch.bfloat16):
+                seed: int = 0, device="cpu", bias_dtype=torch.bfloat16, dtype=torch.bfloat16):
     """(q [1,H,m,d], k [1,H,n,d], v [1,H,n,d], bias [1,H,1,n]) for the biased attention.
 
-    bias = log(counts) cast to the q dtype and expanded to every head, the
-    layout vggt/layers/attention.py:259-260 hands to the kernel.
+    q, k and v are N(0, 1/d) rounded once to `dtype` (bf16 or fp16); bias =
+    log(counts) cast to `bias_dtype` (the q dtype in the model) and
+    expanded to every head, the layout vggt/layers/attention.py:259-260
+    hands to the kernel.
     """
     g = _gen(device, seed)
     s = 1.0 / math.sqrt(d)
-    q = (torch.randn(1, heads, m, d, generator=g, device=device) * s).to(torch.bfloat16)
-    k = (torch.randn(1, heads, n, d, generator=g, device=device) * s).to(torch.bfloat16)
-    v = (torch.randn(1, heads, n, d, generator=g, device=device) * s).to(torch.bfloat16)
+    q = (torch.randn(1, heads, m, d, generator=g, device=device) * s).to(dtype)
+    k = (torch.randn(1, heads, n, d, generator=g, device=device) * s).to(dtype)
+    v = (torch.randn(1, heads, n, d, generator=g, device=device) * s).to(dtype)
     counts = merge_counts(m, n, seed=seed, device=device)
     bias = counts.log().to(bias_dtype).reshape(1, 1, 1, n).expand(1, heads, 1, n).contiguous()
     return q, k, v, bias

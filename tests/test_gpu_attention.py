@@ -22,6 +22,15 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS = 2e-2, 5e-3
 LSE_TOL = 2.0 ** -8 / 0.6931471805599453 + 1e-5
+# The full-size workload's outputs are ~1e-4 (v ~ N(0, 1/64) averaged over
+# 10^4-10^5 keys), where the absolute bar says little: those tests also hold
+# the worst row's |o - ref|_2 / |ref|_2 (bf16 rounding of P and of the output
+# gives ~2^-9 per element).
+ROW_REL = 2e-2
+
+
+def _worst_row_rel(got, ref):
+    return ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
 
 
 def _inputs(B, H, M, N, seed, qk_scale=0.5, bias="bf16"):
@@ -274,9 +283,13 @@ def test_full_size_attention_workload(dev):
     rows = torch.cat([torch.arange(64), torch.randint(64, 274_800, (64,), generator=g),
                       torch.arange(274_800 - 64, 274_800)])
     ref, _ = attention_reference(q[:, :, rows.to(dev)].cpu(), k.cpu(), v.cpu(), bias.cpu(), 0.125)
-    err = (o[:, :, rows.to(dev)].float().cpu() - ref).abs()
-    print(f"\n[attn c3] sample max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e}")
+    got = o[:, :, rows.to(dev)].float().cpu()
+    err = (got - ref).abs()
+    rel = _worst_row_rel(got, ref)
+    print(f"\n[attn c3] sample max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e} "
+          f"worst row relative {rel:.2e}")
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    assert rel <= ROW_REL
 
 
 def test_full_size_sharp_logits_mix_offsets(dev):
@@ -309,10 +322,13 @@ def test_full_size_sharp_logits_mix_offsets(dev):
                       torch.nonzero(~sharp).view(-1).cpu()[torch.randperm(int((~sharp).sum()),
                                                                            generator=cpu)[:48]]])
     ref, _ = attention_reference(q[:, :, rows.to(dev)].cpu(), k.cpu(), v.cpu(), bias.cpu(), 0.125)
-    err = (o[:, :, rows.to(dev)].float().cpu() - ref).abs()
+    got = o[:, :, rows.to(dev)].float().cpu()
+    err = (got - ref).abs()
+    rel = _worst_row_rel(got, ref)
     print(f"[attn c3 sharp] sample max-abs {err.max().item():.3e} mean-abs "
-          f"{err.mean().item():.3e}", flush=True)
+          f"{err.mean().item():.3e} worst row relative {rel:.2e}", flush=True)
     assert err.max().item() <= MAX_ABS and err.mean().item() <= 2e-3
+    assert rel <= ROW_REL
 
 
 def _aligned_inputs(M, N, X, planted, seed, dtype):

@@ -163,5 +163,12 @@ def test_200_frame_shapes_on_a_sample(dev):
                           frames=frames, rows=rows)
     yc = y.float().cpu().view(B, S, P, H, 64)
     for f in frames:
-        err = (yc[:, f, rows].permute(0, 2, 1, 3) - ref[f]).abs()
+        got = yc[:, f, rows].permute(0, 2, 1, 3)
+        err = (got - ref[f]).abs()
+        # Outputs here are ~1e-2 (v ~ N(0, 1/64)): each row is also held to
+        # its own scale, |y - ref|_2 / |ref|_2.
+        rel = ((got - ref[f]).norm(dim=-1) / ref[f].norm(dim=-1)).max().item()
+        print(f"[frame special 200f] frame {f}: max-abs {err.max().item():.2e}, worst row "
+              f"relative {rel:.2e}", flush=True)
         assert err.max().item() <= 2e-2 and err.mean().item() <= 5e-3, (f, err.max())
+        assert rel <= 2e-2, (f, rel)
