@@ -55,6 +55,8 @@ def _check(o, ref, tight=True):
     err = (o.float().cpu() - ref).abs()
     assert err.max().item() <= MAX_ABS, err.max().item()
     assert err.mean().item() <= (2e-3 if tight else MEAN_ABS), err.mean().item()
+    rel = _worst_row_rel(o.float().cpu(), ref)
+    assert rel <= ROW_REL, rel
 
 
 @pytest.mark.parametrize("B,H,M,N", [
@@ -400,6 +402,7 @@ def test_tile0_offset_layernorm_scale(dev, dtype):
     ref, ref_lse = attention_reference(q, k, v, b, 0.125)
     err = (o.float().cpu() - ref).abs()
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    assert _worst_row_rel(o.float().cpu(), ref) <= ROW_REL
     f = flags.cpu()
     if dtype == torch.float16:
         assert ((f == 0) | (f == _native.ATTN_FLAG_TILE0)).all()

@@ -51,6 +51,9 @@ def _check(dev, q, k, v, b, D, tight=True):
     err = (o.float().cpu() - ref).abs()
     assert err.max().item() <= MAX_ABS, err.max().item()
     assert err.mean().item() <= (MEAN_ABS if tight else 5e-3), err.mean().item()
+    # each row at its own scale too: |o - ref|_2 / |ref|_2 (16-bit P and output)
+    rel = ((o.float().cpu() - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
+    assert rel <= 2e-2, rel
     assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL
     return o
 

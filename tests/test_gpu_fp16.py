@@ -33,6 +33,12 @@ from oracle.attention import attention_reference
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS = 2e-2, 5e-3
+
+
+def _worst_row_rel(o, ref):
+    """Largest |o - ref|_2 / |ref|_2 over the rows: each row at its own scale."""
+    got = o.float().cpu()
+    return ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
 LSE_TOL16 = 2.0 ** -10 / 0.6931471805599453 + 1e-5
 
 
@@ -124,6 +130,7 @@ def test_attention_f16_matches_reference_and_beats_bf16(dev, B, H, M, N, with_bi
     assert o16.dtype == torch.float16 and l16.dtype == torch.float32
     err16 = (o16.float().cpu() - ref).abs()
     assert err16.max().item() <= MAX_ABS and err16.mean().item() <= MEAN_ABS
+    assert _worst_row_rel(o16, ref) <= 2e-2
     assert (l16.cpu() - ref_lse).abs().max().item() < LSE_TOL16
     obf, _ = _run(q, k, v, bias, torch.bfloat16, dev)
     errbf = (obf.float().cpu() - ref).abs()
@@ -156,6 +163,7 @@ def test_attention_f16_fixed_and_lazy_offset_waves_mix(dev, lse):
     ref, ref_lse = attention_reference(q, k, v, bias, 0.125)
     err = (o.float().cpu() - ref).abs()
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    assert _worst_row_rel(o, ref) <= 2e-2
     if lse:
         assert (out[1].cpu() - ref_lse).abs().max().item() < LSE_TOL16
     _, _, flags = _native.attn_keybias_offset_flags(
@@ -182,6 +190,7 @@ def test_attention_f16_increasing_logits_rescale(dev):
     err = (o.float().cpu() - ref).abs()
     assert torch.isfinite(o).all()
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    assert _worst_row_rel(o, ref) <= 2e-2
     assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL16
 
 
@@ -201,6 +210,7 @@ def test_attention_f16_row_max_at_the_bound(dev):
     assert torch.isfinite(o).all() and torch.isfinite(lse).all()
     err = (o.float().cpu() - ref).abs()
     assert err.max().item() <= MAX_ABS and err.mean().item() <= MEAN_ABS
+    assert _worst_row_rel(o, ref) <= 2e-2
     assert (lse.cpu() - ref_lse).abs().max().item() < LSE_TOL16
 
 
